@@ -1,0 +1,809 @@
+// g4_api.hip -- the C ABI declared in include/g4hip.h.
+//
+// Host-side argument validation (the error conventions of the reference's
+// tensor layer mapped to status codes), contexts, weight upload and the
+// dispatch of each entry point onto the kernels of g4_kernels.hip.  Reference
+// paths are relative to lib/src/main/kotlin/io/github/lbenedetto/internal/.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/g4hip.h"
+#include "g4_internal.hpp"
+
+struct g4_ctx {
+  int device;
+  hipStream_t own_stream;
+  hipStream_t stream;
+  g4::DevInfo dev;
+  char *scratch;  // grow-only device buffer for staging and intermediates
+  size_t scratch_bytes;
+  float *am_val;  // argmax partials, counter (kept at zero between launches) and result
+  int32_t *am_idx;
+  uint32_t *am_counter;
+  int32_t *am_out;
+};
+
+struct g4_weight {
+  int device;
+  int type;
+  int64_t n_elems;
+  int64_t nbytes;
+  uint8_t *d;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() { return G4_OK; }
+
+int hip_fail(hipError_t e, const char *what) {
+  if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+    return fail(G4_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
+  return fail(G4_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define G4_HIP(call, what)                 \
+  do {                                     \
+    hipError_t _e = (call);                \
+    if (_e != hipSuccess) return hip_fail(_e, what); \
+  } while (0)
+
+// GGMLType.kt:16-30 for the supported ids.
+bool type_info(int t, int *bs, int *ts) {
+  switch (t) {
+    case G4_TYPE_F32: *bs = 1; *ts = 4; return true;
+    case G4_TYPE_F16: *bs = 1; *ts = 2; return true;
+    case G4_TYPE_BF16: *bs = 1; *ts = 2; return true;
+    case G4_TYPE_Q4_0: *bs = 32; *ts = 18; return true;
+    case G4_TYPE_Q8_0: *bs = 32; *ts = 34; return true;
+    case G4_TYPE_Q4_K: *bs = 256; *ts = 144; return true;
+    default: return false;
+  }
+}
+
+constexpr size_t ALIGN = 256;
+size_t up(size_t n) { return (n + ALIGN - 1) & ~(ALIGN - 1); }
+
+int use_device(g4_ctx *ctx) {
+  G4_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  return G4_OK;
+}
+
+// Make sure the context's scratch holds `bytes`; waits for queued work before a regrow.
+int ensure_scratch(g4_ctx *ctx, size_t bytes) {
+  if (bytes <= ctx->scratch_bytes) return G4_OK;
+  G4_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (ctx->scratch) G4_HIP(hipFree(ctx->scratch), "hipFree");
+  ctx->scratch = nullptr;
+  ctx->scratch_bytes = 0;
+  size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+  void *p = nullptr;
+  G4_HIP(hipMalloc(&p, want), "hipMalloc(scratch)");
+  ctx->scratch = (char *)p;
+  ctx->scratch_bytes = want;
+  return G4_OK;
+}
+
+// Bump allocator over the scratch: layout computed first, then carved.
+struct Carve {
+  size_t off = 0;
+  size_t add(size_t bytes) {
+    size_t o = off;
+    off += up(bytes);
+    return o;
+  }
+};
+
+int check_ctx(const g4_ctx *ctx) {
+  if (!ctx) return fail(G4_ERR_INVALID_ARGUMENT, "context is null");
+  return G4_OK;
+}
+
+int check_weight(const g4_ctx *ctx, const g4_weight *w, const char *name) {
+  if (!w) return fail(G4_ERR_INVALID_ARGUMENT, "%s is null", name);
+  if (w->device != ctx->device)
+    return fail(G4_ERR_INVALID_ARGUMENT, "%s lives on device %d, context on device %d", name, w->device,
+                ctx->device);
+  return G4_OK;
+}
+
+// FloatTensor.kt:18-29: rows this_offset + i*dim1 .. + dim1 for i < dim0 must lie in the tensor.
+int check_geometry(int64_t n_elems, int64_t this_offset, int32_t dim0, int32_t dim1) {
+  if (dim0 < 0 || dim1 < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative dims (%d, %d)", dim0, dim1);
+  if (this_offset < 0) return fail(G4_ERR_OUT_OF_RANGE, "negative offset %lld", (long long)this_offset);
+  const int64_t need = this_offset + (int64_t)dim0 * dim1;
+  if (need > n_elems)
+    return fail(G4_ERR_OUT_OF_RANGE, "offset %lld + %d x %d elements exceeds the tensor's %lld",
+                (long long)this_offset, dim0, dim1, (long long)n_elems);
+  return G4_OK;
+}
+
+int check_rows(const g4_weight *w, int64_t this_offset, int32_t dim0, int32_t dim1) {
+  return check_geometry(w->n_elems, this_offset, dim0, dim1);
+}
+
+g4::RowsArgs plain_rows(const g4_weight *w, int64_t this_offset, const float *x, float *y, int32_t dim0,
+                        int32_t dim1) {
+  g4::RowsArgs a;
+  memset(&a, 0, sizeof(a));
+  a.W0 = a.W1 = w->d;
+  a.base0 = a.base1 = this_offset;
+  a.row_stride = dim1;
+  a.expert_stride = 0;
+  a.ids = nullptr;
+  a.expert_count = 1;
+  a.rows = dim0;
+  a.dim1 = dim1;
+  a.x = x;
+  a.x_stride = 0;
+  a.x_div = 1;
+  a.y = y;
+  a.y_stride = 0;
+  return a;
+}
+
+int launch_status(hipError_t e, const char *what) {
+  if (e == hipErrorInvalidValue) return fail(G4_ERR_INVALID_ARGUMENT, "%s: unsupported launch shape", what);
+  if (e != hipSuccess) return hip_fail(e, what);
+  return G4_OK;
+}
+
+int copy_in(g4_ctx *ctx, void *dst, const void *src, size_t bytes) {
+  if (bytes) G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync(H2D)");
+  return G4_OK;
+}
+
+int copy_out(g4_ctx *ctx, void *dst, const void *src, size_t bytes) {
+  if (bytes) G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync(D2H)");
+  return G4_OK;
+}
+
+int finish(g4_ctx *ctx) {
+  G4_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return G4_OK;
+}
+
+#define G4_TRY(expr)        \
+  do {                      \
+    int _rc = (expr);       \
+    if (_rc != G4_OK) return _rc; \
+  } while (0)
+
+// --- shared bodies of host and device entry points ---
+
+int matmul_dev(g4_ctx *ctx, const g4_weight *w, int64_t off, const float *d_x, float *d_y, int32_t dim0,
+               int32_t dim1) {
+  if (dim0 == 0) return G4_OK;
+  if (dim1 == 0) {
+    G4_HIP(hipMemsetAsync(d_y, 0, sizeof(float) * (size_t)dim0, ctx->stream), "hipMemsetAsync");
+    return G4_OK;
+  }
+  g4::RowsArgs a = plain_rows(w, off, d_x, d_y, dim0, dim1);
+  return launch_status(g4::launch_rows(w->type, g4::EPI_STORE, a, 1, ctx->dev, nullptr, ctx->stream), "matmul");
+}
+
+int batch_dev(g4_ctx *ctx, const g4_weight *w, int64_t off, const float *d_X, int32_t M, float *d_Y, int32_t dim0,
+              int32_t dim1) {
+  if (dim0 == 0 || M == 0) return G4_OK;
+  if (dim1 == 0) {
+    G4_HIP(hipMemsetAsync(d_Y, 0, sizeof(float) * (size_t)dim0 * M, ctx->stream), "hipMemsetAsync");
+    return G4_OK;
+  }
+  g4::RowsArgs a = plain_rows(w, off, d_X, d_Y, dim0, dim1);
+  a.x_stride = dim1;
+  a.y_stride = dim0;
+  return launch_status(g4::launch_rows(w->type, g4::EPI_STORE, a, M, ctx->dev, nullptr, ctx->stream),
+                       "matmul_batch");
+}
+
+int argmax_rows_dev(g4_ctx *ctx, const g4_weight *w, int64_t off, const float *d_x, float *d_logits,
+                    int32_t *d_index, int32_t dim0, int32_t dim1) {
+  g4::RowsArgs a = plain_rows(w, off, d_x, d_logits, dim0, dim1);
+  a.am_val = ctx->am_val;
+  a.am_idx = ctx->am_idx;
+  a.am_counter = ctx->am_counter;
+  a.am_out = d_index;
+  return launch_status(g4::launch_rows(w->type, g4::EPI_ARGMAX, a, 1, ctx->dev, nullptr, ctx->stream),
+                       "matmul_argmax");
+}
+
+int ffn_dev(g4_ctx *ctx, const g4_weight *wg, const g4_weight *wu, const g4_weight *wd, const float *d_x,
+            float *d_y, float *d_h, float *d_gu, int32_t dim, int32_t hidden) {
+  g4::RowsArgs a = plain_rows(wg, 0, d_x, d_h, hidden, dim);
+  a.W1 = wu->d;
+  G4_TRY(launch_status(g4::launch_rows(wg->type, g4::EPI_GELU_PAIR, a, 1, ctx->dev, d_gu, ctx->stream), "ffn"));
+  g4::RowsArgs b = plain_rows(wd, 0, d_h, d_y, dim, hidden);
+  return launch_status(g4::launch_rows(wd->type, g4::EPI_STORE, b, 1, ctx->dev, nullptr, ctx->stream), "ffn");
+}
+
+int check_ffn(g4_ctx *ctx, const g4_weight *wg, const g4_weight *wu, const g4_weight *wd, int32_t dim,
+              int32_t hidden) {
+  G4_TRY(check_weight(ctx, wg, "w_gate"));
+  G4_TRY(check_weight(ctx, wu, "w_up"));
+  G4_TRY(check_weight(ctx, wd, "w_down"));
+  if (dim <= 0 || hidden <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "ffn dims must be positive (%d, %d)", dim, hidden);
+  G4_TRY(check_rows(wg, 0, hidden, dim));
+  G4_TRY(check_rows(wu, 0, hidden, dim));
+  G4_TRY(check_rows(wd, 0, dim, hidden));
+  if (wg->type != wu->type) return fail(G4_ERR_UNSUPPORTED, "ffn: gate and up weights must share one GGML type");
+  return G4_OK;
+}
+
+int check_moe(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t T, int32_t dim, int32_t ff,
+              int32_t k, int32_t *n_experts) {
+  G4_TRY(check_weight(ctx, wgu, "w_gate_up"));
+  G4_TRY(check_weight(ctx, wdn, "w_down"));
+  if (T < 0 || k < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative T or k (%d, %d)", T, k);
+  if (dim <= 0 || ff <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "moe dims must be positive (%d, %d)", dim, ff);
+  const int64_t per_gu = 2 * (int64_t)ff * dim, per_dn = (int64_t)dim * ff;
+  if (wgu->n_elems % per_gu != 0)
+    return fail(G4_ERR_INVALID_ARGUMENT, "w_gate_up holds %lld elements, not a multiple of 2*ff*dim = %lld",
+                (long long)wgu->n_elems, (long long)per_gu);
+  const int64_t ne = wgu->n_elems / per_gu;
+  if (wdn->n_elems < ne * per_dn)
+    return fail(G4_ERR_OUT_OF_RANGE, "w_down holds %lld elements, %lld experts need %lld", (long long)wdn->n_elems,
+                (long long)ne, (long long)(ne * per_dn));
+  if (ne > 0x7fffffff) return fail(G4_ERR_INVALID_ARGUMENT, "too many experts");
+  *n_experts = (int32_t)ne;
+  return G4_OK;
+}
+
+int moe_dev(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t n_experts, const float *d_X, int32_t T,
+            int32_t dim, int32_t ff, const int32_t *d_ids, const float *d_w, int32_t k, float *d_Y, float *d_h,
+            float *d_ys, float *d_gu) {
+  const int32_t S = T * k;  // (token, slot) pairs
+  if (S == 0) {
+    if (T > 0) G4_HIP(hipMemsetAsync(d_Y, 0, sizeof(float) * (size_t)T * dim, ctx->stream), "hipMemsetAsync");
+    return G4_OK;
+  }
+  g4::RowsArgs a;
+  memset(&a, 0, sizeof(a));
+  a.W0 = a.W1 = wgu->d;
+  a.base0 = 0;
+  a.base1 = (int64_t)ff * dim;
+  a.row_stride = dim;
+  a.expert_stride = 2 * (int64_t)ff * dim;
+  a.ids = d_ids;
+  a.expert_count = n_experts;
+  a.rows = ff;
+  a.dim1 = dim;
+  a.x = d_X;
+  a.x_stride = dim;
+  a.x_div = k;
+  a.y = d_h;
+  a.y_stride = ff;
+  G4_TRY(launch_status(g4::launch_rows(wgu->type, g4::EPI_GELU_PAIR, a, S, ctx->dev, d_gu, ctx->stream), "moe"));
+  g4::RowsArgs b;
+  memset(&b, 0, sizeof(b));
+  b.W0 = b.W1 = wdn->d;
+  b.row_stride = ff;
+  b.expert_stride = (int64_t)dim * ff;
+  b.ids = d_ids;
+  b.expert_count = n_experts;
+  b.rows = dim;
+  b.dim1 = ff;
+  b.x = d_h;
+  b.x_stride = ff;
+  b.x_div = 1;
+  b.y = d_ys;
+  b.y_stride = dim;
+  G4_TRY(launch_status(g4::launch_rows(wdn->type, g4::EPI_STORE, b, S, ctx->dev, nullptr, ctx->stream), "moe"));
+  return launch_status(g4::launch_moe_combine(d_ys, d_w, T, k, dim, d_Y, ctx->stream), "moe");
+}
+
+size_t moe_scratch(int32_t T, int32_t dim, int32_t ff, int32_t k, Carve &c, size_t *h, size_t *ys, size_t *gu) {
+  const size_t S = (size_t)T * k;
+  *h = c.add(sizeof(float) * S * ff);
+  *ys = c.add(sizeof(float) * S * dim);
+  *gu = c.add(sizeof(float) * S * 2 * ff);
+  return c.off;
+}
+
+}  // namespace
+
+// =============================================================== C ABI ====
+
+extern "C" {
+
+const char *g4_last_error(void) { return g_last_error.c_str(); }
+
+int g4_version(void) { return (0 << 16) | 1; }
+
+int g4_device_count(int *count) {
+  if (!count) return fail(G4_ERR_INVALID_ARGUMENT, "count is null");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e == hipErrorNoDevice || e == hipErrorInsufficientDriver || e == hipErrorInitializationError) n = 0;
+  else if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  *count = n;
+  (void)hipGetLastError();
+  return G4_OK;
+}
+
+int g4_type_info(int ggml_type, int *block_size, int *type_size) {
+  int bs, ts;
+  if (!type_info(ggml_type, &bs, &ts)) return fail(G4_ERR_UNSUPPORTED, "Quantization format %d", ggml_type);
+  if (block_size) *block_size = bs;
+  if (type_size) *type_size = ts;
+  return G4_OK;
+}
+
+int g4_byte_size(int ggml_type, int64_t n_elems, int64_t *nbytes) {
+  int bs, ts;
+  if (!type_info(ggml_type, &bs, &ts)) return fail(G4_ERR_UNSUPPORTED, "Quantization format %d", ggml_type);
+  if (!nbytes) return fail(G4_ERR_INVALID_ARGUMENT, "nbytes is null");
+  if (n_elems < 0 || n_elems % bs != 0)
+    return fail(G4_ERR_INVALID_ARGUMENT, "%lld elements is not a whole number of %d-element blocks",
+                (long long)n_elems, bs);
+  *nbytes = n_elems / bs * ts;
+  return G4_OK;
+}
+
+int g4_check_matmul(int ggml_type, int64_t n_elems, int64_t this_offset, int32_t dim0, int32_t dim1) {
+  int bs, ts;
+  if (!type_info(ggml_type, &bs, &ts)) return fail(G4_ERR_UNSUPPORTED, "Quantization format %d", ggml_type);
+  if (n_elems < 0 || n_elems % bs != 0)
+    return fail(G4_ERR_INVALID_ARGUMENT, "%lld elements is not a whole number of %d-element blocks",
+                (long long)n_elems, bs);
+  return check_geometry(n_elems, this_offset, dim0, dim1);
+}
+
+int g4_open(int ordinal, g4_ctx **out) {
+  if (!out) return fail(G4_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  int n = 0;
+  G4_TRY(g4_device_count(&n));
+  if (n == 0) return fail(G4_ERR_NO_DEVICE, "no HIP device is present");
+  if (ordinal < 0 || ordinal >= n) return fail(G4_ERR_NO_DEVICE, "device %d does not exist (%d present)", ordinal, n);
+  G4_HIP(hipSetDevice(ordinal), "hipSetDevice");
+  g4_ctx *c = new g4_ctx();
+  memset(c, 0, sizeof(*c));
+  c->device = ordinal;
+  int cu = 0;
+  hipError_t e = hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, ordinal);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_fail(e, "hipDeviceGetAttribute");
+  }
+  c->dev.cu_count = cu > 0 ? cu : 1;
+  e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_fail(e, "hipStreamCreate");
+  }
+  c->stream = c->own_stream;
+  const int nb = g4::max_argmax_blocks(c->dev);
+  void *p = nullptr;
+  size_t bytes = up(sizeof(float) * nb) + up(sizeof(int32_t) * nb) + up(sizeof(uint32_t)) + up(sizeof(int32_t));
+  e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) {
+    (void)hipStreamDestroy(c->own_stream);
+    delete c;
+    return hip_fail(e, "hipMalloc(argmax)");
+  }
+  char *b = (char *)p;
+  c->am_val = (float *)b;
+  c->am_idx = (int32_t *)(b + up(sizeof(float) * nb));
+  c->am_counter = (uint32_t *)(b + up(sizeof(float) * nb) + up(sizeof(int32_t) * nb));
+  c->am_out = (int32_t *)((char *)c->am_counter + up(sizeof(uint32_t)));
+  e = hipMemset(p, 0, bytes);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    (void)hipStreamDestroy(c->own_stream);
+    delete c;
+    return hip_fail(e, "hipMemset");
+  }
+  *out = c;
+  return G4_OK;
+}
+
+int g4_close(g4_ctx *ctx) {
+  G4_TRY(check_ctx(ctx));
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipStreamSynchronize(ctx->own_stream);
+  if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->am_val) (void)hipFree(ctx->am_val);
+  (void)hipStreamDestroy(ctx->own_stream);
+  delete ctx;
+  return G4_OK;
+}
+
+int g4_ctx_set_stream(g4_ctx *ctx, void *stream) {
+  G4_TRY(check_ctx(ctx));
+  ctx->stream = stream ? (hipStream_t)stream : ctx->own_stream;
+  return G4_OK;
+}
+
+int g4_ctx_sync(g4_ctx *ctx) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(use_device(ctx));
+  return finish(ctx);
+}
+
+int g4_ctx_device(const g4_ctx *ctx, int *ordinal) {
+  G4_TRY(check_ctx(ctx));
+  if (!ordinal) return fail(G4_ERR_INVALID_ARGUMENT, "ordinal is null");
+  *ordinal = ctx->device;
+  return G4_OK;
+}
+
+int g4_upload(g4_ctx *ctx, int ggml_type, const void *raw, int64_t nbytes, int64_t n_elems, g4_weight **out) {
+  G4_TRY(check_ctx(ctx));
+  if (!out) return fail(G4_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  int bs, ts;
+  if (!type_info(ggml_type, &bs, &ts)) return fail(G4_ERR_UNSUPPORTED, "Quantization format %d", ggml_type);
+  if (n_elems < 0 || n_elems % bs != 0)
+    return fail(G4_ERR_INVALID_ARGUMENT, "%lld elements is not a whole number of %d-element blocks",
+                (long long)n_elems, bs);
+  const int64_t want = n_elems / bs * ts;
+  if (nbytes != want)
+    return fail(G4_ERR_INVALID_ARGUMENT, "nbytes %lld != byteSizeFor(%lld) = %lld", (long long)nbytes,
+                (long long)n_elems, (long long)want);
+  if (!raw && nbytes > 0) return fail(G4_ERR_INVALID_ARGUMENT, "raw is null");
+  G4_TRY(use_device(ctx));
+  void *d = nullptr;
+  const size_t alloc = (size_t)nbytes + ALIGN;  // zeroed tail: no load ever reads past a block, kept as margin
+  G4_HIP(hipMalloc(&d, alloc), "hipMalloc(weight)");
+  hipError_t e = hipMemsetAsync((char *)d + nbytes, 0, ALIGN, ctx->stream);
+  if (e == hipSuccess && nbytes > 0) e = hipMemcpyAsync(d, raw, (size_t)nbytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    return hip_fail(e, "upload");
+  }
+  g4_weight *w = new g4_weight();
+  w->device = ctx->device;
+  w->type = ggml_type;
+  w->n_elems = n_elems;
+  w->nbytes = nbytes;
+  w->d = (uint8_t *)d;
+  *out = w;
+  return G4_OK;
+}
+
+int g4_weight_free(g4_weight *w) {
+  if (!w) return fail(G4_ERR_INVALID_ARGUMENT, "weight is null");
+  int cur = 0;
+  (void)hipGetDevice(&cur);
+  (void)hipSetDevice(w->device);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(w->d);
+  (void)hipSetDevice(cur);
+  delete w;
+  return G4_OK;
+}
+
+int g4_weight_info(const g4_weight *w, int *ggml_type, int64_t *n_elems, int64_t *nbytes) {
+  if (!w) return fail(G4_ERR_INVALID_ARGUMENT, "weight is null");
+  if (ggml_type) *ggml_type = w->type;
+  if (n_elems) *n_elems = w->n_elems;
+  if (nbytes) *nbytes = w->nbytes;
+  return G4_OK;
+}
+
+int g4_weight_device_ptr(const g4_weight *w, const void **dptr) {
+  if (!w || !dptr) return fail(G4_ERR_INVALID_ARGUMENT, "null argument");
+  *dptr = w->d;
+  return G4_OK;
+}
+
+// ---------------------------------------------------------------- matmul ----
+
+int g4_matmul(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const float *that, float *out, int32_t dim0,
+              int32_t dim1) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_weight(ctx, w, "weight"));
+  G4_TRY(check_rows(w, this_offset, dim0, dim1));
+  if ((!that && dim1 > 0) || (!out && dim0 > 0)) return fail(G4_ERR_INVALID_ARGUMENT, "that/out is null");
+  if (dim0 == 0) return ok();
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t ox = c.add(sizeof(float) * (size_t)dim1), oy = c.add(sizeof(float) * (size_t)dim0);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  float *dx = (float *)(ctx->scratch + ox), *dy = (float *)(ctx->scratch + oy);
+  G4_TRY(copy_in(ctx, dx, that, sizeof(float) * (size_t)dim1));
+  G4_TRY(matmul_dev(ctx, w, this_offset, dx, dy, dim0, dim1));
+  G4_TRY(copy_out(ctx, out, dy, sizeof(float) * (size_t)dim0));
+  return finish(ctx);
+}
+
+int g4_matmul_dev(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const float *d_that, float *d_out,
+                  int32_t dim0, int32_t dim1) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_weight(ctx, w, "weight"));
+  G4_TRY(check_rows(w, this_offset, dim0, dim1));
+  if ((!d_that && dim1 > 0) || (!d_out && dim0 > 0)) return fail(G4_ERR_INVALID_ARGUMENT, "that/out is null");
+  G4_TRY(use_device(ctx));
+  return matmul_dev(ctx, w, this_offset, d_that, d_out, dim0, dim1);
+}
+
+int g4_matmul_batch(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const float *X, int32_t M, float *Y,
+                    int32_t dim0, int32_t dim1) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_weight(ctx, w, "weight"));
+  G4_TRY(check_rows(w, this_offset, dim0, dim1));
+  if (M < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative M %d", M);
+  if (M > 65535) return fail(G4_ERR_INVALID_ARGUMENT, "M %d exceeds 65535", M);
+  if ((!X && M > 0 && dim1 > 0) || (!Y && M > 0 && dim0 > 0)) return fail(G4_ERR_INVALID_ARGUMENT, "X/Y is null");
+  if (M == 0 || dim0 == 0) return ok();
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t ox = c.add(sizeof(float) * (size_t)dim1 * M), oy = c.add(sizeof(float) * (size_t)dim0 * M);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  float *dx = (float *)(ctx->scratch + ox), *dy = (float *)(ctx->scratch + oy);
+  G4_TRY(copy_in(ctx, dx, X, sizeof(float) * (size_t)dim1 * M));
+  G4_TRY(batch_dev(ctx, w, this_offset, dx, M, dy, dim0, dim1));
+  G4_TRY(copy_out(ctx, Y, dy, sizeof(float) * (size_t)dim0 * M));
+  return finish(ctx);
+}
+
+int g4_matmul_batch_dev(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const float *d_X, int32_t M,
+                        float *d_Y, int32_t dim0, int32_t dim1) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_weight(ctx, w, "weight"));
+  G4_TRY(check_rows(w, this_offset, dim0, dim1));
+  if (M < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative M %d", M);
+  if (M > 65535) return fail(G4_ERR_INVALID_ARGUMENT, "M %d exceeds 65535", M);
+  if ((!d_X && M > 0 && dim1 > 0) || (!d_Y && M > 0 && dim0 > 0))
+    return fail(G4_ERR_INVALID_ARGUMENT, "X/Y is null");
+  G4_TRY(use_device(ctx));
+  return batch_dev(ctx, w, this_offset, d_X, M, d_Y, dim0, dim1);
+}
+
+// -------------------------------------------------------------- argmax ----
+
+int g4_matmul_argmax(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const float *that, float *logits,
+                     int32_t *index, int32_t dim0, int32_t dim1) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_weight(ctx, w, "weight"));
+  G4_TRY(check_rows(w, this_offset, dim0, dim1));
+  if (dim0 <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "argmax needs dim0 > 0 (FloatTensor.kt:54)");
+  if ((!that && dim1 > 0) || !index) return fail(G4_ERR_INVALID_ARGUMENT, "that/index is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t ox = c.add(sizeof(float) * (size_t)dim1), oy = c.add(sizeof(float) * (size_t)dim0),
+         oi = c.add(sizeof(int32_t));
+  G4_TRY(ensure_scratch(ctx, c.off));
+  float *dx = (float *)(ctx->scratch + ox), *dy = (float *)(ctx->scratch + oy);
+  int32_t *di = (int32_t *)(ctx->scratch + oi);
+  G4_TRY(copy_in(ctx, dx, that, sizeof(float) * (size_t)dim1));
+  if (dim1 == 0) {
+    G4_HIP(hipMemsetAsync(dy, 0, sizeof(float) * (size_t)dim0, ctx->stream), "hipMemsetAsync");
+    G4_TRY(launch_status(g4::launch_argmax(dy, dim0, ctx->am_val, ctx->am_idx, ctx->am_counter, di, ctx->dev,
+                                           ctx->stream), "argmax"));
+  } else {
+    G4_TRY(argmax_rows_dev(ctx, w, this_offset, dx, dy, di, dim0, dim1));
+  }
+  if (logits) G4_TRY(copy_out(ctx, logits, dy, sizeof(float) * (size_t)dim0));
+  G4_TRY(copy_out(ctx, index, di, sizeof(int32_t)));
+  return finish(ctx);
+}
+
+int g4_matmul_argmax_dev(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const float *d_that,
+                         float *d_logits, int32_t *d_index, int32_t dim0, int32_t dim1) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_weight(ctx, w, "weight"));
+  G4_TRY(check_rows(w, this_offset, dim0, dim1));
+  if (dim0 <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "argmax needs dim0 > 0 (FloatTensor.kt:54)");
+  if ((!d_that && dim1 > 0) || !d_index) return fail(G4_ERR_INVALID_ARGUMENT, "that/index is null");
+  G4_TRY(use_device(ctx));
+  float *dy = d_logits;
+  if (!dy) {
+    Carve c;
+    size_t oy = c.add(sizeof(float) * (size_t)dim0);
+    G4_TRY(ensure_scratch(ctx, c.off));
+    dy = (float *)(ctx->scratch + oy);
+  }
+  if (dim1 == 0) {
+    G4_HIP(hipMemsetAsync(dy, 0, sizeof(float) * (size_t)dim0, ctx->stream), "hipMemsetAsync");
+    return launch_status(g4::launch_argmax(dy, dim0, ctx->am_val, ctx->am_idx, ctx->am_counter, d_index, ctx->dev,
+                                           ctx->stream), "argmax");
+  }
+  return argmax_rows_dev(ctx, w, this_offset, d_that, dy, d_index, dim0, dim1);
+}
+
+int g4_argmax(g4_ctx *ctx, const float *v, int32_t n, int32_t *index) {
+  G4_TRY(check_ctx(ctx));
+  if (n <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "argmax needs size > 0 (FloatTensor.kt:54)");
+  if (!v || !index) return fail(G4_ERR_INVALID_ARGUMENT, "v/index is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t ov = c.add(sizeof(float) * (size_t)n), oi = c.add(sizeof(int32_t));
+  G4_TRY(ensure_scratch(ctx, c.off));
+  float *dv = (float *)(ctx->scratch + ov);
+  int32_t *di = (int32_t *)(ctx->scratch + oi);
+  G4_TRY(copy_in(ctx, dv, v, sizeof(float) * (size_t)n));
+  G4_TRY(launch_status(
+      g4::launch_argmax(dv, n, ctx->am_val, ctx->am_idx, ctx->am_counter, di, ctx->dev, ctx->stream), "argmax"));
+  G4_TRY(copy_out(ctx, index, di, sizeof(int32_t)));
+  return finish(ctx);
+}
+
+int g4_argmax_dev(g4_ctx *ctx, const float *d_v, int32_t n, int32_t *d_index) {
+  G4_TRY(check_ctx(ctx));
+  if (n <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "argmax needs size > 0 (FloatTensor.kt:54)");
+  if (!d_v || !d_index) return fail(G4_ERR_INVALID_ARGUMENT, "v/index is null");
+  G4_TRY(use_device(ctx));
+  return launch_status(
+      g4::launch_argmax(d_v, n, ctx->am_val, ctx->am_idx, ctx->am_counter, d_index, ctx->dev, ctx->stream), "argmax");
+}
+
+// ------------------------------------------------------------- dequant ----
+
+int g4_dequant(g4_ctx *ctx, const g4_weight *w, int64_t offset, int64_t n, float *out) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_weight(ctx, w, "weight"));
+  if (n < 0 || offset < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative offset or count");
+  if (offset + n > w->n_elems)
+    return fail(G4_ERR_OUT_OF_RANGE, "elements %lld..%lld exceed the tensor's %lld", (long long)offset,
+                (long long)(offset + n), (long long)w->n_elems);
+  if (!out && n > 0) return fail(G4_ERR_INVALID_ARGUMENT, "out is null");
+  if (n == 0) return ok();
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t oo = c.add(sizeof(float) * (size_t)n);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  float *d = (float *)(ctx->scratch + oo);
+  G4_TRY(launch_status(g4::launch_dequant(w->type, w->d, offset, n, d, ctx->stream), "dequant"));
+  G4_TRY(copy_out(ctx, out, d, sizeof(float) * (size_t)n));
+  return finish(ctx);
+}
+
+int g4_dequant_dev(g4_ctx *ctx, const g4_weight *w, int64_t offset, int64_t n, float *d_out) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_weight(ctx, w, "weight"));
+  if (n < 0 || offset < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative offset or count");
+  if (offset + n > w->n_elems)
+    return fail(G4_ERR_OUT_OF_RANGE, "elements %lld..%lld exceed the tensor's %lld", (long long)offset,
+                (long long)(offset + n), (long long)w->n_elems);
+  if (!d_out && n > 0) return fail(G4_ERR_INVALID_ARGUMENT, "out is null");
+  if (n == 0) return ok();
+  G4_TRY(use_device(ctx));
+  return launch_status(g4::launch_dequant(w->type, w->d, offset, n, d_out, ctx->stream), "dequant");
+}
+
+// ------------------------------------------------------------------ ffn ----
+
+int g4_ffn(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const g4_weight *w_down, const float *x,
+           float *y, int32_t dim, int32_t hidden) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_ffn(ctx, w_gate, w_up, w_down, dim, hidden));
+  if (!x || !y) return fail(G4_ERR_INVALID_ARGUMENT, "x/y is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t ox = c.add(sizeof(float) * (size_t)dim), oy = c.add(sizeof(float) * (size_t)dim),
+         oh = c.add(sizeof(float) * (size_t)hidden), og = c.add(sizeof(float) * 2 * (size_t)hidden);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  float *dx = (float *)(ctx->scratch + ox), *dy = (float *)(ctx->scratch + oy);
+  float *dh = (float *)(ctx->scratch + oh), *dg = (float *)(ctx->scratch + og);
+  G4_TRY(copy_in(ctx, dx, x, sizeof(float) * (size_t)dim));
+  G4_TRY(ffn_dev(ctx, w_gate, w_up, w_down, dx, dy, dh, dg, dim, hidden));
+  G4_TRY(copy_out(ctx, y, dy, sizeof(float) * (size_t)dim));
+  return finish(ctx);
+}
+
+int g4_ffn_dev(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const g4_weight *w_down,
+               const float *d_x, float *d_y, int32_t dim, int32_t hidden) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_ffn(ctx, w_gate, w_up, w_down, dim, hidden));
+  if (!d_x || !d_y) return fail(G4_ERR_INVALID_ARGUMENT, "x/y is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t oh = c.add(sizeof(float) * (size_t)hidden), og = c.add(sizeof(float) * 2 * (size_t)hidden);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  float *dh = (float *)(ctx->scratch + oh), *dg = (float *)(ctx->scratch + og);
+  return ffn_dev(ctx, w_gate, w_up, w_down, d_x, d_y, dh, dg, dim, hidden);
+}
+
+// ------------------------------------------------------------------ moe ----
+
+static int check_route(int32_t T, int32_t n_experts, int32_t k) {
+  if (T < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative T %d", T);
+  if (n_experts <= 0 || n_experts > 1024)
+    return fail(G4_ERR_INVALID_ARGUMENT, "n_experts %d outside 1..1024", n_experts);
+  if (k < 0 || k > n_experts) return fail(G4_ERR_INVALID_ARGUMENT, "k %d outside 0..n_experts", k);
+  return G4_OK;
+}
+
+int g4_moe_route(g4_ctx *ctx, const float *logits, int32_t T, int32_t n_experts, int32_t k, int32_t renormalize,
+                 const float *expert_scale, int32_t *ids, float *weights) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_route(T, n_experts, k));
+  if (T == 0 || k == 0) return ok();
+  if (!logits || !ids || !weights) return fail(G4_ERR_INVALID_ARGUMENT, "logits/ids/weights is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t ol = c.add(sizeof(float) * (size_t)T * n_experts), os = c.add(sizeof(float) * (size_t)n_experts),
+         oi = c.add(sizeof(int32_t) * (size_t)T * k), ow = c.add(sizeof(float) * (size_t)T * k);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  float *dl = (float *)(ctx->scratch + ol), *ds = (float *)(ctx->scratch + os);
+  int32_t *di = (int32_t *)(ctx->scratch + oi);
+  float *dw = (float *)(ctx->scratch + ow);
+  G4_TRY(copy_in(ctx, dl, logits, sizeof(float) * (size_t)T * n_experts));
+  if (expert_scale) G4_TRY(copy_in(ctx, ds, expert_scale, sizeof(float) * (size_t)n_experts));
+  G4_TRY(launch_status(g4::launch_route(dl, T, n_experts, k, renormalize, expert_scale ? ds : nullptr, di, dw,
+                                        ctx->stream), "moe_route"));
+  G4_TRY(copy_out(ctx, ids, di, sizeof(int32_t) * (size_t)T * k));
+  G4_TRY(copy_out(ctx, weights, dw, sizeof(float) * (size_t)T * k));
+  return finish(ctx);
+}
+
+int g4_moe_route_dev(g4_ctx *ctx, const float *d_logits, int32_t T, int32_t n_experts, int32_t k,
+                     int32_t renormalize, const float *d_expert_scale, int32_t *d_ids, float *d_weights) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_route(T, n_experts, k));
+  if (T == 0 || k == 0) return ok();
+  if (!d_logits || !d_ids || !d_weights) return fail(G4_ERR_INVALID_ARGUMENT, "logits/ids/weights is null");
+  G4_TRY(use_device(ctx));
+  return launch_status(
+      g4::launch_route(d_logits, T, n_experts, k, renormalize, d_expert_scale, d_ids, d_weights, ctx->stream),
+      "moe_route");
+}
+
+int g4_moe(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *X, int32_t T, int32_t dim,
+           int32_t ff, const int32_t *ids, const float *weights, int32_t k, float *Y) {
+  G4_TRY(check_ctx(ctx));
+  int32_t ne = 0;
+  G4_TRY(check_moe(ctx, w_gate_up, w_down, T, dim, ff, k, &ne));
+  if (T == 0) return ok();
+  if (!X || !Y || (k > 0 && (!ids || !weights))) return fail(G4_ERR_INVALID_ARGUMENT, "X/Y/ids/weights is null");
+  for (int64_t i = 0; i < (int64_t)T * k; ++i)
+    if (ids[i] < 0 || ids[i] >= ne)
+      return fail(G4_ERR_OUT_OF_RANGE, "expert id %d at %lld outside 0..%d", ids[i], (long long)i, ne - 1);
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t ox = c.add(sizeof(float) * (size_t)T * dim), oi = c.add(sizeof(int32_t) * (size_t)T * k),
+         ow = c.add(sizeof(float) * (size_t)T * k), oy = c.add(sizeof(float) * (size_t)T * dim);
+  size_t oh, oys, ogu;
+  moe_scratch(T, dim, ff, k, c, &oh, &oys, &ogu);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  char *s = ctx->scratch;
+  G4_TRY(copy_in(ctx, s + ox, X, sizeof(float) * (size_t)T * dim));
+  if (k > 0) {
+    G4_TRY(copy_in(ctx, s + oi, ids, sizeof(int32_t) * (size_t)T * k));
+    G4_TRY(copy_in(ctx, s + ow, weights, sizeof(float) * (size_t)T * k));
+  }
+  G4_TRY(moe_dev(ctx, w_gate_up, w_down, ne, (const float *)(s + ox), T, dim, ff, (const int32_t *)(s + oi),
+                 (const float *)(s + ow), k, (float *)(s + oy), (float *)(s + oh), (float *)(s + oys),
+                 (float *)(s + ogu)));
+  G4_TRY(copy_out(ctx, Y, s + oy, sizeof(float) * (size_t)T * dim));
+  return finish(ctx);
+}
+
+int g4_moe_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *d_X, int32_t T,
+               int32_t dim, int32_t ff, const int32_t *d_ids, const float *d_weights, int32_t k, float *d_Y) {
+  G4_TRY(check_ctx(ctx));
+  int32_t ne = 0;
+  G4_TRY(check_moe(ctx, w_gate_up, w_down, T, dim, ff, k, &ne));
+  if (T == 0) return ok();
+  if (!d_X || !d_Y || (k > 0 && (!d_ids || !d_weights)))
+    return fail(G4_ERR_INVALID_ARGUMENT, "X/Y/ids/weights is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t oh, oys, ogu;
+  moe_scratch(T, dim, ff, k, c, &oh, &oys, &ogu);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  char *s = ctx->scratch;
+  return moe_dev(ctx, w_gate_up, w_down, ne, d_X, T, dim, ff, d_ids, d_weights, k, d_Y, (float *)(s + oh),
+                 (float *)(s + oys), (float *)(s + ogu));
+}
+
+}  // extern "C"

@@ -1,0 +1,374 @@
+// g4_device.hpp -- device-side building blocks for gfx950 (CDNA4, wave64).
+//
+// GGUF block decoders (the per-format get() of the reference) and the 64-element
+// "chunk" dot products used by the row-stream matvec kernels.  Reference paths
+// are relative to lib/src/main/kotlin/io/github/lbenedetto/internal/.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define G4_DEV __device__ __forceinline__
+
+namespace g4 {
+
+enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_BF16 = 30 };
+
+// Four dwords at 4-byte alignment: one global_load_dwordx4 (gfx950 needs dword alignment only).
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Hide a value from the optimiser so (v >> 8k) & 0xff selects v_cvt_f32_ubyte{k}
+// instead of being re-fused with an earlier mask into bfe + ubyte0.
+G4_DEV uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// binary16 -> binary32 (v_cvt_f32_f16; fp16 denormals are preserved in the
+// kernels' default float mode, so this is the exact decode of
+// FloatTensorHelpers.kt:39-41).
+G4_DEV float h2f(uint32_t h16) { return __half2float(__ushort_as_half((unsigned short)(h16 & 0xFFFFu))); }
+
+// F16FloatTensor.kt:59-61: the vector path's bit trick (zero exponent -> +-0,
+// exponent 31 -> finite 2^16 * 1.m).
+G4_DEV float h2f_vec(uint32_t h16) {
+  int32_t b = (int32_t)(int16_t)(uint16_t)h16;
+  int32_t mask = (-(b & 0x7C00)) >> 31;
+  uint32_t out = ((uint32_t)(b & 0x8000) << 16) | ((((uint32_t)(b & 0x7FFF) + 0x1C000u) << 13) & (uint32_t)mask);
+  return __uint_as_float(out);
+}
+
+G4_DEV float bf2f(uint32_t h16) { return __uint_as_float((h16 & 0xFFFFu) << 16); }
+
+G4_DEV float sbyte(uint32_t v, int b) { return (float)(int8_t)(v >> (8 * b)); }  // v_cvt_f32_i32_sdwa sext
+G4_DEV float ubyte(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }  // v_cvt_f32_ubyte{b}
+
+G4_DEV uint32_t rd_u8(const uint8_t *p) { return *p; }
+G4_DEV uint32_t rd_u16(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+// Q4_KFloatTensor.kt:70-84 getScaleMinK4.
+G4_DEV int q4k_scale_min(int j, const uint8_t *s, bool is_min) {
+  if (j < 4) return s[is_min ? j + 4 : j] & 63;
+  int low = is_min ? (s[j + 4] >> 4) : (s[j + 4] & 0xF);
+  int high = (s[is_min ? j : j - 4] >> 6) & 0x3;
+  return low | (high << 4);
+}
+
+// Per-element get(index), bit-exact restatement of the reference:
+// Q8_0FloatTensor.kt:21-28, Q4_0FloatTensor.kt:21-39, Q4_KFloatTensor.kt:23-55,
+// F16FloatTensor.kt:20-23, BF16FloatTensor.kt:20-24, F32FloatTensor.kt:18-20.
+// __fmul_rn/__fsub_rn keep each operation separately rounded like the JVM.
+template <int TYPE>
+G4_DEV float get_elem(const uint8_t *W, int64_t idx) {
+  if constexpr (TYPE == T_Q8_0) {
+    const uint8_t *b = W + (idx >> 5) * 34;
+    return __fmul_rn((float)(int8_t)b[2 + (idx & 31)], h2f(rd_u16(b)));
+  } else if constexpr (TYPE == T_Q4_0) {
+    const uint8_t *b = W + (idx >> 5) * 18;
+    int mod = (int)(idx & 31);
+    int q = (mod < 16) ? (b[2 + mod] & 0xF) : (b[2 + mod - 16] >> 4);
+    return __fmul_rn((float)(q - 8), h2f(rd_u16(b)));
+  } else if constexpr (TYPE == T_Q4_K) {
+    const uint8_t *b = W + (idx >> 8) * 144;
+    int within = (int)(idx & 255);
+    int group = within >> 6, in_group = within & 63;
+    int sub = group * 2 + (in_group >= 32 ? 1 : 0);
+    int nib = in_group & 31;
+    int sc = q4k_scale_min(sub, b + 4, false);
+    int m = q4k_scale_min(sub, b + 4, true);
+    int byte = b[16 + group * 32 + nib];
+    int q = (in_group >= 32) ? (byte >> 4) : (byte & 0xF);
+    float d = h2f(rd_u16(b)), dmin = h2f(rd_u16(b + 2));
+    float t = __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
+    return __fsub_rn(t, __fmul_rn(dmin, (float)m));
+  } else if constexpr (TYPE == T_F16) {
+    return h2f(rd_u16(W + idx * 2));
+  } else if constexpr (TYPE == T_BF16) {
+    return bf2f(rd_u16(W + idx * 2));
+  } else {
+    return *(const float *)(W + idx * 4);
+  }
+}
+
+// Element decode used by a dot at row position j of a row of length dim1: the
+// F16 vector path decodes with the bit trick up to loopBound(dim1) = dim1 & ~15
+// and with the exact decode in the scalar tail (F16FloatTensor.kt:43-77).
+template <int TYPE>
+G4_DEV float dot_elem(const uint8_t *W, int64_t idx, int j, int dim1) {
+  if constexpr (TYPE == T_F16) {
+    uint32_t h = rd_u16(W + idx * 2);
+    return j < (dim1 & ~15) ? h2f_vec(h) : h2f(h);
+  } else {
+    return get_elem<TYPE>(W, idx);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 64-element chunks.  A chunk starts at an element offset e that is a multiple
+// of 64 and holds: Q8_0 two blocks (68 B), Q4_0 two blocks (36 B), Q4_K one
+// 64-weight group of a super-block (32 B of nibbles + the 16 B super-block
+// head), F16/BF16 128 B, F32 256 B.  load() issues only dword-aligned vector
+// loads; dot() unpacks in registers against x[0..64) and the precomputed sums.
+// ---------------------------------------------------------------------------
+
+// Q8_0: {fp16 d, int8 q[32]} x 2 = 17 dwords starting dword-aligned (68 * k).
+struct FmtQ8_0 {
+  static constexpr int TYPE = T_Q8_0, NDW = 17, NS = 0, RT = 4;
+  G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
+    const uint8_t *p = W + (e >> 6) * 68;
+    const u32x4a4 *v = (const u32x4a4 *)p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32x4a4 t = v[i];
+      D[4 * i + 0] = t.x; D[4 * i + 1] = t.y; D[4 * i + 2] = t.z; D[4 * i + 3] = t.w;
+    }
+    D[16] = ((const uint32_t *)p)[16];
+  }
+  G4_DEV static void sums(const float *x, float *s) { (void)x; (void)s; }
+  // per block: (sum_k x_k q_k) * d, the scale applied after the block sum like
+  // the reference's fma(s0 + s1, d, acc) (Q8_0FloatTensor.kt:64-78).
+  G4_DEV static float dot(const uint32_t (&D)[NDW], const float *x, const float *s, int64_t e) {
+    (void)s; (void)e;
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t q = __builtin_amdgcn_alignbyte(D[i + 1], D[i], 2);  // bytes 2..33: q of block 0
+#pragma unroll
+      for (int b = 0; b < 4; ++b) a0 = __builtin_fmaf(x[4 * i + b], sbyte(q, b), a0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t q = D[9 + i];  // bytes 36..67: q of block 1 (dword aligned)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) a1 = __builtin_fmaf(x[32 + 4 * i + b], sbyte(q, b), a1);
+    }
+    float d0 = h2f(D[0] & 0xFFFFu), d1 = h2f(D[8] >> 16);
+    return __builtin_fmaf(a0, d0, a1 * d1);
+  }
+};
+
+// Q4_0: {fp16 d, 16 B nibbles} x 2 = 9 dwords (36 * k).  Element k < 16 of a
+// block is the low nibble of byte k, element 16 + k the high nibble; value
+// (q - 8) * d (Q4_0FloatTensor.kt:21-39).  The high nibble is used in place
+// (16 q, exact) and the 1/16 folded into the block sum; -8 enters through the
+// precomputed sum of x.
+struct FmtQ4_0 {
+  static constexpr int TYPE = T_Q4_0, NDW = 9, NS = 2, RT = 4;
+  G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
+    const uint8_t *p = W + (e >> 6) * 36;
+    const u32x4a4 *v = (const u32x4a4 *)p;
+    u32x4a4 t0 = v[0], t1 = v[1];
+    D[0] = t0.x; D[1] = t0.y; D[2] = t0.z; D[3] = t0.w;
+    D[4] = t1.x; D[5] = t1.y; D[6] = t1.z; D[7] = t1.w;
+    D[8] = ((const uint32_t *)p)[8];
+  }
+  G4_DEV static void sums(const float *x, float *s) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) s0 += x[k], s1 += x[32 + k];
+    s[0] = s0; s[1] = s1;
+  }
+  G4_DEV static float block(const uint32_t (&Q)[4], const float *x, float sx) {
+    float lo = 0.f, hi = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t l = opaque(Q[i] & 0x0F0F0F0Fu), h = opaque(Q[i] & 0xF0F0F0F0u);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        lo = __builtin_fmaf(x[4 * i + b], ubyte(l, b), lo);
+        hi = __builtin_fmaf(x[16 + 4 * i + b], ubyte(h, b), hi);
+      }
+    }
+    return __builtin_fmaf(-8.f, sx, __builtin_fmaf(hi, 0.0625f, lo));
+  }
+  G4_DEV static float dot(const uint32_t (&D)[NDW], const float *x, const float *s, int64_t e) {
+    (void)e;
+    uint32_t Q0[4], Q1[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      Q0[i] = __builtin_amdgcn_alignbyte(D[i + 1], D[i], 2);  // bytes 2..17
+      Q1[i] = D[5 + i];                                          // bytes 20..35
+    }
+    float t0 = block(Q0, x, s[0]);
+    float t1 = block(Q1, x + 32, s[1]);
+    return __builtin_fmaf(h2f(D[0] & 0xFFFFu), t0, h2f(D[4] >> 16) * t1);
+  }
+};
+
+// Q4_K: super-block {fp16 d, fp16 dmin, scales[12], qs[128]} (144 B).  Group g
+// (64 weights) uses qs[32g .. 32g+32): low nibbles are sub-block 2g, high
+// nibbles sub-block 2g+1; w = d*sc*q - dmin*m (Q4_KFloatTensor.kt:23-55).
+// Per sub-block: d*sc * sum(x q) - dmin*m * sum(x).
+struct FmtQ4_K {
+  static constexpr int TYPE = T_Q4_K, NDW = 12, NS = 2, RT = 4;
+  G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
+    int64_t G = e >> 6;
+    const uint8_t *sb = W + (G >> 2) * 144;
+    const u32x4 *qs = (const u32x4 *)(sb + 16 + 32 * (int)(G & 3));
+    u32x4 h = *(const u32x4 *)sb, q0 = qs[0], q1 = qs[1];
+    D[0] = q0.x; D[1] = q0.y; D[2] = q0.z; D[3] = q0.w;
+    D[4] = q1.x; D[5] = q1.y; D[6] = q1.z; D[7] = q1.w;
+    D[8] = h.x; D[9] = h.y; D[10] = h.z; D[11] = h.w;
+  }
+  G4_DEV static void sums(const float *x, float *s) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) s0 += x[k], s1 += x[32 + k];
+    s[0] = s0; s[1] = s1;
+  }
+  G4_DEV static float dot(const uint32_t (&D)[NDW], const float *x, const float *s, int64_t e) {
+    float lo = 0.f, hi = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t l = opaque(D[i] & 0x0F0F0F0Fu), h = opaque(D[i] & 0xF0F0F0F0u);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        lo = __builtin_fmaf(x[4 * i + b], ubyte(l, b), lo);
+        hi = __builtin_fmaf(x[32 + 4 * i + b], ubyte(h, b), hi);
+      }
+    }
+    // getScaleMinK4 (Q4_KFloatTensor.kt:70-84) for sub-blocks 2g and 2g+1: both
+    // live in bytes 2(g&1), 2(g&1)+1 of the three scale dwords.
+    const int g = (int)((e >> 6) & 3);
+    const uint32_t sh = (uint32_t)(g & 1) * 16u;
+    const uint32_t y = D[9] >> sh, z = D[10] >> sh, w = D[11] >> sh;
+    uint32_t scp, mp;
+    if (g < 2) {
+      scp = y & 0x3F3Fu;
+      mp = z & 0x3F3Fu;
+    } else {
+      scp = (w & 0x0F0Fu) | ((y >> 2) & 0x3030u);
+      mp = ((w >> 4) & 0x0F0Fu) | ((z >> 2) & 0x3030u);
+    }
+    const float d = h2f(D[8] & 0xFFFFu), dmin = h2f(D[8] >> 16);
+    const float d1 = d * ubyte(scp, 0), d2 = d * ubyte(scp, 1) * 0.0625f;
+    const float m1 = dmin * ubyte(mp, 0), m2 = dmin * ubyte(mp, 1);
+    float r = __builtin_fmaf(d1, lo, -(m1 * s[0]));
+    return __builtin_fmaf(d2, hi, __builtin_fmaf(-m2, s[1], r));
+  }
+};
+
+// F16 / BF16: 64 halves = 32 dwords (16-byte aligned chunks).  F16 uses the
+// vector-path decode (the fast path requires dim1 % 64 == 0, so no element is
+// in the scalar tail); BF16 is exact.
+template <int TYPE_>
+struct FmtHalf {
+  static constexpr int TYPE = TYPE_, NDW = 32, NS = 0, RT = 2;
+  G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
+    const u32x4 *v = (const u32x4 *)(W + e * 2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      u32x4 t = v[i];
+      D[4 * i + 0] = t.x; D[4 * i + 1] = t.y; D[4 * i + 2] = t.z; D[4 * i + 3] = t.w;
+    }
+  }
+  G4_DEV static void sums(const float *x, float *s) { (void)x; (void)s; }
+  G4_DEV static float dot(const uint32_t (&D)[NDW], const float *x, const float *s, int64_t e) {
+    (void)s; (void)e;
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      float w0, w1;
+      if constexpr (TYPE == T_F16) {
+        w0 = h2f_vec(D[i] & 0xFFFFu);
+        w1 = h2f_vec(D[i] >> 16);
+      } else {
+        w0 = __uint_as_float(D[i] << 16);
+        w1 = __uint_as_float(D[i] & 0xFFFF0000u);
+      }
+      a = __builtin_fmaf(w0, x[2 * i], a);
+      b = __builtin_fmaf(w1, x[2 * i + 1], b);
+    }
+    return a + b;
+  }
+};
+
+// F32: 64 floats = 16 dwordx4.
+struct FmtF32 {
+  static constexpr int TYPE = T_F32, NDW = 64, NS = 0, RT = 2;
+  G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
+    const u32x4 *v = (const u32x4 *)(W + e * 4);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      u32x4 t = v[i];
+      D[4 * i + 0] = t.x; D[4 * i + 1] = t.y; D[4 * i + 2] = t.z; D[4 * i + 3] = t.w;
+    }
+  }
+  G4_DEV static void sums(const float *x, float *s) { (void)x; (void)s; }
+  G4_DEV static float dot(const uint32_t (&D)[NDW], const float *x, const float *s, int64_t e) {
+    (void)s; (void)e;
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      a = __builtin_fmaf(__uint_as_float(D[2 * i]), x[2 * i], a);
+      b = __builtin_fmaf(__uint_as_float(D[2 * i + 1]), x[2 * i + 1], b);
+    }
+    return a + b;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Wave reductions.
+// ---------------------------------------------------------------------------
+
+// Sum N values over the LPR lanes of each lane group (LPR a power of two, N <= LPR).
+// The first log2(N) butterfly steps exchange half of the remaining values
+// (a transposing reduction), the rest reduce one value.  On return, lane q of a
+// group holds the group total of value index q / (LPR / N).
+template <int N, int LPR>
+G4_DEV float reduce_transpose(float (&v)[N], int lane) {
+  static_assert((N & (N - 1)) == 0 && (LPR & (LPR - 1)) == 0 && N <= LPR, "powers of two");
+  int n = N;
+#pragma unroll
+  for (int s = LPR / 2; s >= 1; s >>= 1) {
+    if (n > 1) {
+      const bool upper = (lane & s) != 0;
+      const int h = n / 2;
+#pragma unroll
+      for (int j = 0; j < N / 2; ++j) {
+        if (j < h) {
+          float send = upper ? v[j] : v[j + h];
+          float keep = upper ? v[j + h] : v[j];
+          v[j] = keep + __shfl_xor(send, s, 64);
+        }
+      }
+      n = h;
+    } else {
+      v[0] += __shfl_xor(v[0], s, 64);
+    }
+  }
+  return v[0];
+}
+
+G4_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s, 64);
+  return v;
+}
+
+// (value, index) ordering of FloatTensor.argmax (FloatTensor.kt:53-66) for a
+// parallel reduction: larger value wins, equal values go to the lower index.
+// Callers map NaN to -inf (never wins) except at index 0, where it maps to +inf
+// (the sequential scan keeps a NaN first element).
+G4_DEV bool am_better(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
+G4_DEV float am_key(float v, int64_t idx) { return v != v ? (idx == 0 ? __builtin_inff() : -__builtin_inff()) : v; }
+
+G4_DEV void am_wave(float &v, int &i) {
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    float ov = __shfl_xor(v, s, 64);
+    int oi = __shfl_xor(i, s, 64);
+    if (am_better(ov, oi, v, i)) v = ov, i = oi;
+  }
+}
+
+// Llama.kt:23-25 gelu, evaluated in double like the reference.
+G4_DEV float gelu_ref(float xf) {
+  double x = (double)xf;
+  double inner = 0.7978845608028654 * (x + 0.044715 * (x * x * x));
+  return (float)(0.5 * x * (1.0 + tanh(inner)));
+}
+
+}  // namespace g4

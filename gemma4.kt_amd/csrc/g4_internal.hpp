@@ -1,0 +1,63 @@
+// g4_internal.hpp -- launcher interface between the C ABI (g4_api.hip) and the
+// kernels (g4_kernels.hip).  Host-side only types; no torch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace g4 {
+
+enum Epi : int { EPI_STORE = 0, EPI_ARGMAX = 1, EPI_GELU_PAIR = 2 };
+
+// One "rows" launch: logical rows of one or two matrices dotted against x.
+// Segment s (blockIdx.y) uses expert ids[s] (when ids != null), activation
+// x + (s / x_div) * x_stride and output y + s * y_stride.  Matrix m row r of
+// segment s starts at element base_m + ids[s] * expert_stride + r * row_stride.
+struct RowsArgs {
+  const uint8_t *W0;
+  const uint8_t *W1;
+  int64_t base0;
+  int64_t base1;
+  int64_t row_stride;
+  int64_t expert_stride;
+  const int32_t *ids;
+  int32_t expert_count;  // ids outside [0, expert_count) give zero rows
+  int32_t rows;
+  int32_t dim1;
+  const float *x;
+  int64_t x_stride;
+  int32_t x_div;
+  float *y;
+  int64_t y_stride;
+  // EPI_ARGMAX: per-block partials, arrival counter (zero between launches), result
+  float *am_val;
+  int32_t *am_idx;
+  uint32_t *am_counter;
+  int32_t *am_out;
+};
+
+// Device facts used for launch sizing.
+struct DevInfo {
+  int cu_count;
+};
+
+// True when rows of (type, offsets, dim1) take the 64-element chunk kernels.
+bool rows_fast_ok(int type, const RowsArgs &a, bool paired);
+
+// Launch the matvec engine over `segments` segments.  For EPI_GELU_PAIR the
+// launch writes h[r] = gelu(W0 row r . x) * (W1 row r . x); on the generic path
+// that needs `scratch` of 2 * rows * segments floats.  For EPI_ARGMAX, segments
+// must be 1 and am_* point to at least max_argmax_blocks() partials.
+hipError_t launch_rows(int type, int epi, const RowsArgs &a, int segments, const DevInfo &dev, float *scratch,
+                       hipStream_t stream);
+int max_argmax_blocks(const DevInfo &dev);
+
+hipError_t launch_dequant(int type, const uint8_t *W, int64_t offset, int64_t n, float *out, hipStream_t stream);
+hipError_t launch_argmax(const float *v, int32_t n, float *part_val, int32_t *part_idx, uint32_t *counter,
+                         int32_t *out, const DevInfo &dev, hipStream_t stream);
+hipError_t launch_route(const float *logits, int32_t T, int32_t n_experts, int32_t k, int32_t renorm,
+                        const float *expert_scale, int32_t *ids, float *weights, hipStream_t stream);
+hipError_t launch_moe_combine(const float *ys, const float *weights, int32_t T, int32_t k, int32_t dim, float *Y,
+                              hipStream_t stream);
+
+}  // namespace g4

@@ -1,0 +1,122 @@
+"""CPU checks of the C ABI (no GPU): the library loads, exports every symbol the
+header declares, and the host-side validation maps each failure to the status
+code / exception of the reference's tensor layer."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "g4hip.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(g4_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    syms = header_symbols()
+    for must in ["g4_open", "g4_close", "g4_upload", "g4_matmul", "g4_matmul_dev", "g4_matmul_batch",
+                 "g4_matmul_argmax", "g4_dequant", "g4_ffn", "g4_moe_route", "g4_moe", "g4_last_error"]:
+        assert must in syms
+
+
+def test_library_exports_every_header_symbol(g4):
+    L = g4.lib()
+    out = subprocess.run(["nm", "-D", "--defined-only", g4.LIB_PATH], stdout=subprocess.PIPE, text=True).stdout
+    exported = set(re.findall(r"\bT (g4_\w+)$", out, flags=re.M))
+    for s in header_symbols():
+        assert s in exported, s
+        assert hasattr(L, s)
+    # the Python binding declares a signature for each of them
+    assert set(g4.SIGNATURES) == set(header_symbols())
+
+
+def test_no_device_here(g4):
+    assert g4.device_count() == 0
+    with pytest.raises(g4.IllegalStateException):
+        g4.Context(0)
+    h = ctypes.c_void_p()
+    assert g4.lib().g4_open(0, ctypes.byref(h)) == -4
+    assert "no HIP device" in g4.last_error()
+
+
+def test_type_table(g4):
+    # GGMLType.kt:16-30
+    expect = {0: (1, 4), 1: (1, 2), 2: (32, 18), 8: (32, 34), 12: (256, 144), 30: (1, 2)}
+    for t, (bs, ts) in expect.items():
+        assert g4.GGMLType(t).block_size == bs and g4.GGMLType(t).type_size == ts
+    assert g4.GGMLType.Q8_0.byte_size_for(2048 * 2048) == 4456448
+    assert g4.GGMLType.Q4_0.byte_size_for(8192 * 2048) == 9437184
+    assert g4.GGMLType.Q4_K.byte_size_for(8192 * 2048) == 9437184
+
+
+@pytest.mark.parametrize("bad", [3, 6, 7, 9, 13, 14, 39, 41, -1])
+def test_unsupported_type_ids(g4, bad):
+    with pytest.raises(g4.UnsupportedOperationException):
+        g4.check_matmul(bad, 1024, 0, 1, 1024)
+    bs = ctypes.c_int32()
+    assert g4.lib().g4_type_info(bad, ctypes.byref(bs), None) == -2
+
+
+def test_byte_size_rejects_partial_blocks(g4):
+    with pytest.raises(g4.IllegalArgumentException):
+        g4.GGMLType.Q4_K.byte_size_for(300)
+    with pytest.raises(g4.IllegalArgumentException):
+        g4.GGMLType.Q8_0.byte_size_for(-32)
+
+
+def test_geometry_validation(g4):
+    n = 64 * 2048
+    g4.check_matmul(8, n, 0, 64, 2048)
+    g4.check_matmul(8, n, 2048, 63, 2048)
+    g4.check_matmul(8, n, 0, 0, 2048)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        g4.check_matmul(8, n, 1, 64, 2048)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        g4.check_matmul(8, n, -32, 1, 32)
+    with pytest.raises(g4.IllegalArgumentException):
+        g4.check_matmul(8, n, 0, -1, 2048)
+    with pytest.raises(g4.IllegalArgumentException):
+        g4.check_matmul(8, 33, 0, 1, 32)
+    # offsets past the reference's Int range are representable (int64)
+    g4.check_matmul(0, 3 << 31, (1 << 32), 2, 1 << 20)
+
+
+def test_null_arguments(g4):
+    L = g4.lib()
+    assert L.g4_close(None) == -1
+    assert L.g4_matmul(None, None, 0, None, None, 1, 1) == -1
+    assert L.g4_upload(None, 8, None, 0, 0, None) == -1
+    assert L.g4_weight_free(None) == -1
+    assert L.g4_device_count(None) == -1
+    assert L.g4_moe(None, None, None, None, 1, 1, 1, None, None, 1, None) == -1
+    assert L.g4_argmax(None, None, 1, None) == -1
+    assert "null" in g4.last_error()
+
+
+def test_last_error_is_thread_local(g4):
+    import threading
+    g4.lib().g4_close(None)
+    seen = {}
+
+    def other():
+        seen["msg"] = g4.last_error()
+
+    th = threading.Thread(target=other)
+    th.start()
+    th.join()
+    assert seen["msg"] == "" and "null" in g4.last_error()
+
+
+def test_python_errors_map_to_reference_exceptions(g4):
+    assert issubclass(g4.UnsupportedOperationException, NotImplementedError)
+    assert issubclass(g4.IndexOutOfBoundsException, IndexError)
+    assert issubclass(g4.IllegalArgumentException, ValueError)
+    with pytest.raises(g4.IllegalArgumentException):
+        g4._f32(np.zeros(3, np.float64), "x")

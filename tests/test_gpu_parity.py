@@ -1,0 +1,323 @@
+"""GPU parity of libg4hip.so against the CPU oracle.
+
+Bars (written into each check):
+  * dequantised weights (get): bit-exact fp32;
+  * every dot product: |y - exact| <= 1e-5 * sum|w_i x_i| (+1e-30), exact = fp64 sum
+    over the exactly dequantised weights (the reference's restated vectorDot meets
+    the same bound, tests/test_oracle_pins.py);
+  * argmax indices, routing ids and routing weights: exact.
+"""
+import numpy as np
+import pytest
+
+import synth
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4_0, Q4_K, F16, BF16, F32 = 8, 2, 12, 1, 30, 0
+ALL = [Q8_0, Q4_0, Q4_K, F16, BF16, F32]
+TOL = 1e-5
+
+
+def same_bits(a, b) -> bool:
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    an, bn = np.isnan(a), np.isnan(b)
+    return bool(np.array_equal(an, bn) and np.array_equal(a.view(np.uint32)[~an], b.view(np.uint32)[~bn]))
+
+
+def assert_dots(y, exact, absum, what=""):
+    y = np.asarray(y, np.float64)
+    err = np.abs(y - exact)
+    bound = TOL * absum + 1e-30
+    bad = np.nonzero(err > bound)[0]
+    assert bad.size == 0, "%s: %d rows out of tolerance, first %d: y=%r exact=%r bound=%r" % (
+        what, bad.size, bad[0], y[bad[0]], exact[bad[0]], bound[bad[0]])
+
+
+def upload(g4, ctx, t, raw, n):
+    return g4.FloatTensorFactory.create(ctx, t, raw, n)
+
+
+# ----------------------------------------------------------------- dequant ---
+
+@pytest.mark.parametrize("t", ALL)
+def test_dequant_bit_exact(g4, ctx, oracle, t):
+    announce("dequant type=%d" % t)
+    n = 256 * 96
+    raw = synth.weights(41, "dq%d" % t, t, n)
+    w = upload(g4, ctx, t, raw, n)
+    assert same_bits(w.dequant(0, n), oracle.dequant(t, raw, 0, n))
+    assert same_bits(w.dequant(77, 1000), oracle.dequant(t, raw, 77, 1000))
+    assert same_bits([w.get(5), w.get(n - 1)], [oracle.get(t, raw, 5), oracle.get(t, raw, n - 1)])
+
+
+def test_dequant_every_fp16_scale(g4, ctx, oracle):
+    """All 65536 fp16 patterns as Q8_0 scales with q = 1 and q = -3: w = q * d."""
+    announce("dequant fp16 scales")
+    nb = 65536
+    blk = np.zeros((nb, 34), np.uint8)
+    blk[:, 0:2] = np.arange(nb, dtype=np.uint32).astype(np.uint16).view(np.uint8).reshape(nb, 2)
+    blk[:, 2] = 1
+    blk[:, 3] = np.uint8(0xFD)  # -3
+    raw = blk.reshape(-1)
+    w = upload(g4, ctx, Q8_0, raw, nb * 32)
+    got = w.dequant(0, nb * 32).reshape(nb, 32)
+    want = oracle.dequant(Q8_0, raw, 0, nb * 32).reshape(nb, 32)
+    assert same_bits(got[:, :2], want[:, :2])
+    d = np.arange(nb, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    assert same_bits(got[:, 0], d)
+
+
+def test_dequant_f16_every_pattern(g4, ctx, oracle):
+    announce("dequant f16 patterns")
+    raw = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    w = upload(g4, ctx, F16, raw, 65536)
+    assert same_bits(w.dequant(0, 65536), oracle.fp16_to_f32_array(raw))
+
+
+# ------------------------------------------------------------------ matmul ---
+
+SHAPES = [
+    # (dim0, dim1, this_offset_rows, description)
+    (64, 2048, 0, "aligned 2048"),
+    (37, 1024, 3, "aligned 1024, odd rows, row offset"),
+    (19, 8192, 1, "multi-pass 8192"),
+    (24, 1408, 1, "1408 (Q4_K rows straddle super-blocks)"),
+    (9, 640, 0, "short rows (16-lane groups)"),
+]
+
+
+@pytest.mark.parametrize("t", ALL)
+@pytest.mark.parametrize("shape", SHAPES, ids=[s[3] for s in SHAPES])
+def test_matmul_fast_path(g4, ctx, oracle, t, shape):
+    dim0, dim1, roff, _ = shape
+    announce("matmul type=%d shape=%r" % (t, shape))
+    n = (dim0 + roff + 1) * dim1
+    n = (n + 255) // 256 * 256
+    raw = synth.weights(42, "mm%d.%d" % (t, dim1), t, n)
+    x = synth.activations(42, "x%d" % dim1, dim1)
+    w = upload(g4, ctx, t, raw, n)
+    off = roff * dim1
+    y = np.empty(dim0, np.float32)
+    w.matmul(x, y, dim0, dim1, off)
+    ex, ab = oracle.matmul_exact(t, raw, x, dim0, dim1, off)
+    assert_dots(y, ex, ab, "type %d %r" % (t, shape))
+    ref = oracle.matmul(t, raw, x, dim0, dim1, off)
+    assert_dots(ref, ex, ab, "oracle")
+
+
+GENERIC = [(5, 1000, 7), (3, 33, 1), (4, 2048, 32), (2, 96, 64 + 32), (6, 17, 0), (1, 5, 250)]
+
+
+@pytest.mark.parametrize("t", ALL)
+@pytest.mark.parametrize("g", GENERIC, ids=[str(g) for g in GENERIC])
+def test_matmul_unaligned_offsets(g4, ctx, oracle, t, g):
+    """Offsets / lengths off the 64-element grid (the reference's scalar head/tail)."""
+    dim0, dim1, off = g
+    announce("matmul generic type=%d %r" % (t, g))
+    n = ((off + dim0 * dim1 + 511) // 256) * 256
+    raw = synth.weights(43, "gen%d" % t, t, n)
+    x = synth.activations(43, "xg", dim1)
+    w = upload(g4, ctx, t, raw, n)
+    y = np.empty(dim0, np.float32)
+    w.matmul(x, y, dim0, dim1, off)
+    ex, ab = oracle.matmul_exact(t, raw, x, dim0, dim1, off)
+    assert_dots(y, ex, ab, "generic %d %r" % (t, g))
+
+
+def test_matmul_f16_vector_decode_semantics(g4, ctx, oracle):
+    """Subnormal / non-finite fp16 weights: the dot follows the vector path's
+    decode for j < dim1 & ~15 and the exact decode in the tail (F16FloatTensor.kt:43-77)."""
+    announce("f16 special weights")
+    dim1 = 64 + 20
+    wts = np.full(2 * dim1, 0x3C00, np.uint16)  # 1.0
+    wts[5] = 0x0001                             # subnormal inside the vector part -> 0
+    wts[dim1 - 2] = 0x0003                      # subnormal in the tail -> exact
+    wts[dim1 + 7] = 0x7C00                      # +inf in the vector part -> 65536
+    x = np.ones(dim1, np.float32)
+    w = upload(g4, ctx, F16, wts, 2 * dim1)
+    y = np.empty(2, np.float32)
+    w.matmul(x, y, 2, dim1)
+    exp0 = (dim1 - 2) + 3 * 2.0 ** -24  # 82 ones, one flushed subnormal, one exact tail subnormal
+    exp1 = (dim1 - 1) + 65536.0
+    assert abs(y[0] - exp0) <= TOL * dim1 and abs(y[1] - exp1) <= TOL * (dim1 + 65536)
+    ref = oracle.matmul(F16, wts, x, 2, dim1)
+    assert abs(ref[0] - exp0) <= TOL * dim1 and abs(ref[1] - exp1) <= TOL * (dim1 + 65536)
+
+
+def test_matmul_dev_matches_host(g4, ctx, oracle):
+    import torch
+    announce("matmul_dev")
+    dim0, dim1 = 128, 2048
+    raw = synth.weights(44, "dev", Q4_0, dim0 * dim1)
+    x = synth.activations(44, "x", dim1)
+    w = upload(g4, ctx, Q4_0, raw, dim0 * dim1)
+    y = np.empty(dim0, np.float32)
+    w.matmul(x, y, dim0, dim1)
+    xd = torch.from_numpy(x).cuda()
+    yd = torch.empty(dim0, dtype=torch.float32, device="cuda")
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    try:
+        w.matmul_dev(xd, yd, dim0, dim1)
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_stream(None)
+    assert same_bits(yd.cpu().numpy(), y)
+
+
+def test_range_errors_on_device(g4, ctx):
+    announce("range errors")
+    raw = synth.weights(45, "err", Q8_0, 64 * 32)
+    w = upload(g4, ctx, Q8_0, raw, 64 * 32)
+    x = np.zeros(64, np.float32)
+    y = np.zeros(64, np.float32)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        w.matmul(x, y, 33, 64)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        w.matmul(x, y, 32, 64, 1)
+    with pytest.raises(g4.IllegalArgumentException):
+        g4.FloatTensorFactory.create(ctx, Q8_0, raw[:100], 64 * 32)
+    with pytest.raises(g4.UnsupportedOperationException):
+        g4.FloatTensorFactory.create(ctx, 13, raw, 64 * 32)
+
+
+# -------------------------------------------------------------- workloads ---
+
+def test_q8_0_matvec_2048(g4, ctx, oracle):
+    announce("workload q8_0 matvec 2048x2048")
+    c = synth.q8_0_matvec_2048()
+    w = upload(g4, ctx, Q8_0, c["w"], 2048 * 2048)
+    y = np.empty(2048, np.float32)
+    w.matmul(c["x"], y, 2048, 2048)
+    ex, ab = oracle.matmul_exact(Q8_0, c["w"], c["x"], 2048, 2048)
+    assert_dots(y, ex, ab, "q8_0 2048")
+
+
+def _ffn_reference(oracle, c):
+    dim, hidden = c["dim"], c["hidden"]
+    gu = np.concatenate([c["gate"], c["up"]])
+    ids = np.zeros((1, 1), np.int32)
+    one = np.ones((1, 1), np.float32)
+    y64, bound = oracle.moe_exact(Q4_0, gu, Q4_0, c["down"], c["x"].reshape(1, dim), ids, one, dim, hidden)
+    return y64[0], bound[0]
+
+
+def test_q4_0_ffn_one_token(g4, ctx, oracle):
+    announce("workload q4_0 ffn 8192x2048")
+    c = synth.q4_0_ffn()
+    dim, hidden = c["dim"], c["hidden"]
+    wg = upload(g4, ctx, Q4_0, c["gate"], hidden * dim)
+    wu = upload(g4, ctx, Q4_0, c["up"], hidden * dim)
+    wd = upload(g4, ctx, Q4_0, c["down"], dim * hidden)
+    y = g4.ffn(ctx, wg, wu, wd, c["x"], dim, hidden)
+    y64, bound = _ffn_reference(oracle, c)
+    assert_dots(y, y64, bound, "ffn")
+    # each matvec on its own too
+    g = np.empty(hidden, np.float32)
+    wg.matmul(c["x"], g, hidden, dim)
+    ex, ab = oracle.matmul_exact(Q4_0, c["gate"], c["x"], hidden, dim)
+    assert_dots(g, ex, ab, "gate")
+
+
+def test_q8_0_lm_head_argmax(g4, ctx, oracle):
+    announce("workload q8_0 lm head 262144x2048 + argmax")
+    c = synth.q8_0_lm_head()
+    V, D = c["dim0"], c["dim1"]
+    w = upload(g4, ctx, Q8_0, c["w"], V * D)
+    logits = np.empty(V, np.float32)
+    idx = w.matmul_argmax(c["x"], V, D, logits=logits)
+    ex, ab = oracle.matmul_exact(Q8_0, c["w"], c["x"], V, D)
+    assert_dots(logits, ex, ab, "lm head")
+    # the argmax of the GPU's own logits is the sequential-scan argmax of them
+    assert idx == oracle.argmax(logits)
+    # and equals the exact argmax: the top-1/top-2 gap exceeds both error bounds
+    order = np.argsort(-ex, kind="stable")
+    gap = ex[order[0]] - ex[order[1]]
+    assert gap > 2 * TOL * max(ab[order[0]], ab[order[1]]), "fixture gap too small to pin the argmax"
+    assert idx == int(order[0])
+    # index-only call (logits not returned)
+    assert w.matmul_argmax(c["x"], V, D) == idx
+
+
+@pytest.mark.parametrize("m", [1, 8, 32, 64])
+def test_q4_k_batched(g4, ctx, oracle, m):
+    announce("workload q4_k batched M=%d" % m)
+    c = synth.q4_k_batched(m)
+    R, D = c["dim0"], c["dim1"]
+    w = upload(g4, ctx, Q4_K, c["w"], R * D)
+    Y = w.matmul_batch(c["x"], R, D)
+    rows = np.arange(R) if m <= 8 else np.random.default_rng(m).choice(R, 512, replace=False)
+    for i in range(m):
+        ex, ab = oracle.matmul_exact(Q4_K, c["w"], c["x"][i], R, D)
+        assert_dots(Y[i][rows], ex[rows], ab[rows], "batched m=%d row %d" % (m, i))
+
+
+@pytest.mark.parametrize("tokens", [1, 16])
+@pytest.mark.parametrize("renorm", [True, False])
+def test_moe_route_exact(g4, ctx, oracle, tokens, renorm):
+    announce("moe route T=%d renorm=%s" % (tokens, renorm))
+    lg = synth.activations(46, "route%d" % tokens, tokens * 128).reshape(tokens, 128)
+    scale = None if renorm else np.linspace(0.5, 1.5, 128).astype(np.float32)
+    ids, w = g4.moe_route(ctx, lg, 8, renorm, scale)
+    rids, rw = oracle.route(lg, 8, renorm, scale)
+    assert np.array_equal(ids, rids)
+    assert same_bits(w, rw)
+
+
+@pytest.mark.parametrize("tokens", [1, 16])
+def test_moe_q4_k(g4, ctx, oracle, tokens):
+    announce("workload moe q4_k T=%d" % tokens)
+    c = synth.moe_q4_k(tokens)
+    E, D, FF, K = c["n_experts"], c["dim"], c["ff"], c["k"]
+    wgu = upload(g4, ctx, Q4_K, c["gate_up"], E * 2 * FF * D)
+    wdn = upload(g4, ctx, Q4_K, c["down"], E * D * FF)
+    ids, gw = g4.moe_route(ctx, c["logits"], K, True)
+    rids, rw = oracle.route(c["logits"], K, True)
+    assert np.array_equal(ids, rids) and same_bits(gw, rw)
+    Y = g4.moe(ctx, wgu, wdn, c["x"], ids, gw, D, FF)
+    y64, bound = oracle.moe_exact(Q4_K, c["gate_up"], Q4_K, c["down"], c["x"], rids, rw, D, FF)
+    assert_dots(Y.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe T=%d" % tokens)
+
+
+def test_moe_reference_gates(g4, ctx, oracle):
+    """Un-renormalised gates times a per-expert down scale, as Llama.kt:300-337 uses them."""
+    announce("moe reference gates")
+    E, D, FF, K, T = 16, 512, 256, 4, 3
+    gu = synth.q8_0(47, "gu", E * 2 * FF * D)
+    dn = synth.q8_0(47, "dn", E * D * FF)
+    lg = synth.activations(47, "lg", T * E).reshape(T, E)
+    X = synth.activations(47, "X", T * D).reshape(T, D)
+    scale = np.linspace(0.25, 2.0, E).astype(np.float32)
+    wgu = upload(g4, ctx, Q8_0, gu, E * 2 * FF * D)
+    wdn = upload(g4, ctx, Q8_0, dn, E * D * FF)
+    ids, gw = g4.moe_route(ctx, lg, K, False, scale)
+    Y = g4.moe(ctx, wgu, wdn, X, ids, gw, D, FF)
+    y64, bound = oracle.moe_exact(Q8_0, gu, Q8_0, dn, X, ids, gw, D, FF)
+    assert_dots(Y.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe ref gates")
+    y32 = oracle.moe(Q8_0, gu, Q8_0, dn, X, ids, gw, D, FF)
+    assert_dots(y32.reshape(-1), y64.reshape(-1), bound.reshape(-1), "oracle moe")
+
+
+# ------------------------------------------------------------------ argmax ---
+
+@pytest.mark.parametrize("case", ["ties", "nan_first", "nan_later", "neg_inf", "signed_zero", "random_big"])
+def test_argmax_cases(g4, ctx, oracle, case):
+    announce("argmax %s" % case)
+    rng = np.random.default_rng(8)
+    v = rng.standard_normal(300000).astype(np.float32)
+    if case == "ties":
+        v[1234] = v[99999] = v[250000] = 50.0
+    elif case == "nan_first":
+        v[0] = np.nan
+        v[7] = 100.0
+    elif case == "nan_later":
+        v[5] = np.nan
+        v[200000] = 60.0
+    elif case == "neg_inf":
+        v[:] = -np.inf
+    elif case == "signed_zero":
+        v[:] = -1.0
+        v[1000] = -0.0
+        v[2000] = 0.0
+    assert g4.argmax(ctx, v) == oracle.argmax(v)

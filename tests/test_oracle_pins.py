@@ -1,0 +1,301 @@
+"""Pins of the CPU oracle (oracle/g4_oracle.c) against what the mathematics and
+independent implementations fix.  The reference ships no golden vectors for this
+path, so each oracle function is checked against:
+  * numpy / torch conversions over every 16-bit pattern (fp16, bf16);
+  * a second, independent numpy restatement of the block layouts (tests/npref.py)
+    and hand-derived known answers;
+  * fp64 brute force for every dot product;
+  * closed-form special cases (argmax ties/NaN, softmax, top-k, gelu).
+Mutation checks at the end show the comparisons catch the plausible mistakes
+(nibble order, scale/min swap, dropped head/tail)."""
+import numpy as np
+import pytest
+import torch
+
+import npref
+import synth
+
+Q8_0, Q4_0, Q4_K, F16, BF16, F32 = 8, 2, 12, 1, 30, 0
+ALL = [Q8_0, Q4_0, Q4_K, F16, BF16, F32]
+
+
+def same_bits(a: np.ndarray, b: np.ndarray) -> bool:
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    an, bn = np.isnan(a), np.isnan(b)
+    return bool(np.array_equal(an, bn) and np.array_equal(a.view(np.uint32)[~an], b.view(np.uint32)[~bn]))
+
+
+# ---------------------------------------------------------- 16-bit floats ---
+
+def test_fp16_decode_all_patterns(oracle):
+    h = np.arange(65536, dtype=np.uint32)
+    ours = oracle.fp16_to_f32_array(h)
+    ref = h.astype(np.uint16).view(np.float16).astype(np.float32)
+    assert same_bits(ours, ref)
+    # payload of NaNs kept exactly (Float.float16ToFloat keeps the significand bits)
+    nan = (h >> 10 & 0x1F) == 0x1F
+    nan &= (h & 0x3FF) != 0
+    assert np.array_equal(ours.view(np.uint32)[nan] & 0x7FFFFF, (h[nan] & 0x3FF) << 13)
+
+
+def test_fp16_vector_decode_closed_form(oracle):
+    # F16FloatTensor.kt:59-61: exponent 0 -> signed zero, exponent 31 -> 2^16 * (1 + m/1024), else IEEE.
+    h = np.arange(65536, dtype=np.uint32)
+    ours = oracle.fp16_vec_decode_array(h)
+    e, m, s = (h >> 10) & 0x1F, h & 0x3FF, (h >> 15) & 1
+    sign = np.where(s == 1, -1.0, 1.0)
+    expect = np.where(e == 0, sign * 0.0,
+                      np.where(e == 31, sign * np.ldexp(1.0 + m / 1024.0, 16),
+                               h.astype(np.uint16).view(np.float16).astype(np.float64))).astype(np.float32)
+    assert same_bits(ours, expect)
+    assert np.array_equal(np.signbit(ours), s == 1)
+
+
+def test_bf16_decode_all_patterns(oracle):
+    h = np.arange(65536, dtype=np.int64)
+    ours = oracle.dequant(BF16, h.astype(np.uint16), 0, 65536)
+    ref = torch.from_numpy(h.astype(np.uint16).view(np.int16)).view(torch.bfloat16).float().numpy()
+    assert same_bits(ours, ref)
+
+
+# ------------------------------------------------------------- dequant ---
+
+def _random_blocks(t, n_elems, seed=7):
+    return synth.weights(seed, "pin%d" % t, t, n_elems)
+
+
+@pytest.mark.parametrize("t", ALL)
+def test_dequant_matches_numpy_restatement(oracle, t):
+    n = 256 * 40
+    raw = _random_blocks(t, n)
+    assert same_bits(oracle.dequant(t, raw, 0, n), npref.dequant(t, raw))
+    # get() at arbitrary indices equals the bulk decode
+    idx = np.random.default_rng(3).integers(0, n, 200)
+    assert same_bits([oracle.get(t, raw, int(i)) for i in idx], npref.dequant(t, raw)[idx])
+
+
+def test_q8_0_known_values(oracle):
+    # d = 0.5 (0x3800), q = -127..127 sampled: w = q * d exactly
+    q = np.array(list(range(-127, -111)) + list(range(112, 128)), dtype=np.int8)
+    blk = np.concatenate([np.array([0x00, 0x38], np.uint8), q.view(np.uint8)])
+    assert same_bits(oracle.dequant(Q8_0, blk, 0, 32), q.astype(np.float32) * 0.5)
+
+
+def test_q4_0_known_values(oracle):
+    # low nibbles 0..15 -> elements 0..15, high nibbles 15..0 -> elements 16..31; d = 2.0 (0x4000)
+    qs = np.array([(i & 0xF) | ((15 - i) << 4) for i in range(16)], np.uint8)
+    blk = np.concatenate([np.array([0x00, 0x40], np.uint8), qs])
+    expect = np.array([(i - 8) * 2.0 for i in range(16)] + [((15 - i) - 8) * 2.0 for i in range(16)], np.float32)
+    assert same_bits(oracle.dequant(Q4_0, blk, 0, 32), expect)
+
+
+# hand-derived from the 12-byte layout (bytes 0..3: sc0..3 low 6 bits, top 2 bits
+# = sc4..7 >> 4; bytes 4..7: m0..3 and top bits of m4..7; bytes 8..11: sc4..7 low
+# nibble | m4..7 low nibble << 4)
+Q4K_SCALES_KAT = np.array([0xC1, 0x02, 0x43, 0x84, 0x05, 0xC6, 0x07, 0x48, 0x21, 0x43, 0x65, 0x87], np.uint8)
+Q4K_SC_KAT = [1, 2, 3, 4, 49, 3, 21, 39]
+Q4K_M_KAT = [5, 6, 7, 8, 2, 52, 6, 24]
+
+
+def test_q4k_scale_min_known_answer(oracle):
+    assert [oracle.q4k_scale_min(j, Q4K_SCALES_KAT, False) for j in range(8)] == Q4K_SC_KAT
+    assert [oracle.q4k_scale_min(j, Q4K_SCALES_KAT, True) for j in range(8)] == Q4K_M_KAT
+
+
+def test_q4k_scale_min_roundtrip_all_pairs(oracle):
+    # every (sc, m) value in every one of the 8 positions, packed by the quantizer direction
+    rng = np.random.default_rng(11)
+    for rep in range(64):
+        sc = rng.integers(0, 64, (1, 8))
+        m = rng.integers(0, 64, (1, 8))
+        sc[0, rep % 8] = rep  # sweep 0..63 through each slot
+        m[0, (rep + 3) % 8] = 63 - rep
+        packed = npref.pack_q4k_scales_quantizer(sc, m)[0]
+        assert [oracle.q4k_scale_min(j, packed, False) for j in range(8)] == list(sc[0])
+        assert [oracle.q4k_scale_min(j, packed, True) for j in range(8)] == list(m[0])
+    # the synthetic generator's packer writes the same bytes
+    sc = rng.integers(0, 64, (50, 8))
+    m = rng.integers(0, 64, (50, 8))
+    assert np.array_equal(synth.pack_q4k_scales(sc, m), npref.pack_q4k_scales_quantizer(sc, m))
+
+
+def _q4k_block(d, dmin, sc, m, q):
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([d], np.float16).view(np.uint8)
+    blk[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    blk[4:16] = npref.pack_q4k_scales_quantizer(np.array([sc]), np.array([m]))[0]
+    q = np.asarray(q).reshape(4, 2, 32)
+    blk[16:] = (q[:, 0, :] | (q[:, 1, :] << 4)).reshape(-1).astype(np.uint8)
+    return blk
+
+
+@pytest.mark.parametrize("case", ["extremes", "zero_d", "subnormal_d", "random"])
+def test_q4k_known_values(oracle, case):
+    rng = np.random.default_rng(5)
+    if case == "extremes":
+        d, dmin, sc, m = 0.0625, 0.125, [0, 63, 0, 63, 63, 0, 63, 0], [63, 0, 63, 0, 0, 63, 0, 63]
+        q = np.tile(np.array([0, 15] * 16), 8)
+    elif case == "zero_d":
+        d, dmin, sc, m = 0.0, 0.25, list(range(8)), list(range(60, 68 - 0))[:8]
+        m = [60, 61, 62, 63, 1, 2, 3, 4]
+        q = rng.integers(0, 16, 256)
+    elif case == "subnormal_d":
+        d, dmin, sc, m = 2.0 ** -20, 2.0 ** -22, [63] * 8, [1] * 8
+        q = rng.integers(0, 16, 256)
+    else:
+        d, dmin = 0.0123, 0.0071
+        sc, m = list(rng.integers(0, 64, 8)), list(rng.integers(0, 64, 8))
+        q = rng.integers(0, 16, 256)
+    blk = _q4k_block(d, dmin, sc, m, q)
+    d32 = np.float32(np.float16(d))
+    dm32 = np.float32(np.float16(dmin))
+    sub = np.repeat(np.arange(8), 32)
+    expect = (np.float32(d32) * np.array(sc, np.float32)[sub]) * np.asarray(q, np.float32) - \
+        (np.float32(dm32) * np.array(m, np.float32)[sub])
+    assert same_bits(oracle.dequant(Q4_K, blk, 0, 256), expect.astype(np.float32))
+
+
+# ----------------------------------------------------------------- dots ---
+
+def _offsets(t):
+    bs = {Q8_0: 32, Q4_0: 32, Q4_K: 256}.get(t, 1)
+    # aligned rows, unaligned heads and tails, shorter than one block, odd sizes
+    return [(0, 2048), (bs, 1024), (7, 900), (max(bs - 3, 1), 5), (3, bs + 9), (0, 17), (64, 1408)]
+
+
+@pytest.mark.parametrize("t", ALL)
+def test_exact_dot_matches_numpy_fp64(oracle, t):
+    n = 256 * 24
+    raw = _random_blocks(t, n, seed=21)
+    x = synth.activations(21, "x", n)
+    w = npref.dequant(t, raw).astype(np.float64)
+    for off, size in _offsets(t):
+        v, a = oracle.exact_dot(t, raw, off, x, size)
+        ref = float(np.dot(w[off:off + size], x[:size].astype(np.float64)))
+        refa = float(np.sum(np.abs(w[off:off + size] * x[:size])))
+        assert abs(v - ref) <= 1e-12 * max(refa, 1e-300)
+        assert abs(a - refa) <= 1e-12 * max(refa, 1e-300)
+
+
+@pytest.mark.parametrize("t", ALL)
+@pytest.mark.parametrize("mode", [0, 1])
+def test_reference_dots_within_tolerance(oracle, t, mode):
+    """The restated vectorDot (mode 0) and scalarDot (mode 1) are within the
+    accumulation-order tolerance 1e-5 * sum|w x| of the exact dot."""
+    n = 256 * 24
+    raw = _random_blocks(t, n, seed=22)
+    x = synth.activations(22, "x", n)
+    for off, size in _offsets(t):
+        v = oracle.vector_dot(t, raw, off, x, size) if mode == 0 else oracle.scalar_dot(t, raw, off, x, size)
+        ex, a = oracle.exact_dot(t, raw, off, x, size)
+        assert abs(v - ex) <= 1e-5 * a + 1e-30, (off, size, v, ex, a)
+
+
+def test_vector_dot_f16_uses_vector_decode_then_exact_tail(oracle):
+    # a subnormal fp16 weight is flushed inside loopBound(size) and kept in the tail
+    w = np.zeros(20, np.uint16)
+    w[3] = 0x0001   # 2^-24, inside the first 16 lanes
+    w[18] = 0x0001  # in the scalar tail (size 20 -> loopBound 16)
+    x = np.full(20, 2.0 ** 20, np.float32)
+    v = oracle.vector_dot(F16, w.view(np.uint8), 0, x, 20)
+    assert v == np.float32(2.0 ** -24 * 2.0 ** 20)  # only the tail element counts
+
+
+def test_matmul_rows_and_offset(oracle):
+    n_rows, dim1 = 12, 512
+    raw = _random_blocks(Q4_K, 40 * 256, seed=23)
+    x = synth.activations(23, "x", dim1)
+    off = 3 * 256
+    out = oracle.matmul(Q4_K, raw, x, n_rows, dim1, this_offset=off, threads=2)
+    for i in range(n_rows):
+        assert out[i] == np.float32(oracle.vector_dot(Q4_K, raw, off + i * dim1, x, dim1))
+
+
+# -------------------------------------------------------- argmax / route ---
+
+def test_argmax_semantics(oracle):
+    assert oracle.argmax(np.array([1, 3, 3, 2], np.float32)) == 1              # first of ties
+    assert oracle.argmax(np.array([-0.0, 0.0], np.float32)) == 0                # -0 == +0
+    assert oracle.argmax(np.array([np.nan, 5, 6], np.float32)) == 0             # NaN first wins
+    assert oracle.argmax(np.array([1, np.nan, 0.5], np.float32)) == 0           # NaN never wins
+    assert oracle.argmax(np.array([-np.inf, -np.inf], np.float32)) == 0
+    assert oracle.argmax(np.array([-np.inf, np.inf, np.inf], np.float32)) == 1
+    v = synth.activations(9, "am", 10000)
+    assert oracle.argmax(v) == int(np.argmax(v))
+    assert oracle.argmax(v, 100, 500) == 100 + int(np.argmax(v[100:600]))
+
+
+def test_softmax_matches_fp64(oracle):
+    v = synth.activations(10, "sm", 128)
+    p = oracle.softmax(v)
+    e = np.exp(v.astype(np.float64) - v.max())
+    ref = e / e.sum()
+    assert np.max(np.abs(p - ref)) <= 1e-6 * ref.max()
+    assert abs(float(np.sum(p.astype(np.float64))) - 1.0) < 1e-5
+
+
+def test_topk_order_and_ties(oracle):
+    p = np.array([0.1, 0.3, 0.3, 0.05, 0.25], np.float32)
+    idx, val, masked = oracle.topk(p, 3)
+    assert list(idx) == [1, 2, 4] and list(val) == [np.float32(0.3), np.float32(0.3), np.float32(0.25)]
+    assert np.isneginf(masked[[1, 2, 4]]).all()
+    # more than available: remaining scans see only -inf and keep index 0
+    idx, val, _ = oracle.topk(np.array([0.5, 0.5], np.float32), 3)
+    assert list(idx) == [0, 1, 0] and np.isneginf(val[2])
+    rng = np.random.default_rng(1)
+    for _ in range(20):
+        v = rng.standard_normal(128).astype(np.float32)
+        idx, _, _ = oracle.topk(v, 8)
+        assert list(idx) == list(np.argsort(-v, kind="stable")[:8])
+
+
+def test_route_renormalised_and_scaled(oracle):
+    lg = synth.activations(12, "rt", 4 * 128).reshape(4, 128)
+    ids, w = oracle.route(lg, 8, True)
+    ids0, w0 = oracle.route(lg, 8, False)
+    assert np.array_equal(ids, ids0)
+    for t in range(4):
+        p = oracle.softmax(lg[t])
+        assert list(ids[t]) == list(np.argsort(-p, kind="stable")[:8])
+        assert np.array_equal(w0[t], p[ids[t]])
+        assert abs(float(w[t].astype(np.float64).sum()) - 1.0) < 1e-6
+    scale = np.linspace(0.5, 2.0, 128).astype(np.float32)
+    ids2, w2 = oracle.route(lg, 8, False, scale)
+    assert np.array_equal(w2, w0 * scale[ids0])
+
+
+def test_gelu_matches_torch_tanh_form(oracle):
+    xs = np.linspace(-8, 8, 1001).astype(np.float32)
+    ours = np.array([oracle.gelu(float(v)) for v in xs], np.float32)
+    ref = torch.nn.functional.gelu(torch.from_numpy(xs.astype(np.float64)), approximate="tanh").numpy()
+    # 1 + tanh cancels for x << 0 in double in both forms; compare relative plus a tiny absolute floor
+    assert np.all(np.abs(ours - ref) <= 2e-7 * np.abs(ref) + 1e-12)
+
+
+# ---------------------------------------------------------------- mutations ---
+# The comparisons above must fail for plausible mistakes; plant each mistake in a
+# copy of the numpy restatement and check the oracle disagrees with it.
+
+def test_mutation_nibble_order_detected(oracle):
+    raw = _random_blocks(Q4_0, 32 * 64, seed=31)
+    blk = raw.reshape(-1, 18)
+    d = npref._f16(blk[:, 0:2])
+    swapped = np.concatenate([blk[:, 2:] >> 4, blk[:, 2:] & 0xF], axis=1).astype(np.float32) - 8
+    wrong = (swapped * d[:, None]).reshape(-1)
+    assert not same_bits(oracle.dequant(Q4_0, raw, 0, 32 * 64), wrong)
+
+
+def test_mutation_scale_min_swap_detected(oracle):
+    raw = _random_blocks(Q4_K, 256 * 8, seed=32)
+    sb = raw.reshape(-1, 144).copy()
+    sc, m = npref.q4k_unpack_scales(sb[:, 4:16])
+    sb[:, 4:16] = npref.pack_q4k_scales_quantizer(m, sc)  # scales and mins exchanged
+    assert not same_bits(oracle.dequant(Q4_K, raw, 0, 256 * 8), npref.dequant(Q4_K, sb.reshape(-1)))
+
+
+def test_mutation_dropped_tail_detected(oracle):
+    raw = _random_blocks(Q8_0, 32 * 8, seed=33)
+    x = synth.activations(33, "x", 256)
+    ex, a = oracle.exact_dot(Q8_0, raw, 7, x, 200)
+    dropped, _ = oracle.exact_dot(Q8_0, raw, 7, x, 192)
+    assert abs(dropped - ex) > 1e-5 * a
