@@ -1,0 +1,459 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized matrix-vector path on one MI355X.
+
+Default workload: the Q4_0 FFN of one decode token (gate/up W 8192x2048, down W
+2048x8192, x ~ N(0,1)).  A step is h = gelu(W_gate x) * (W_up x) followed by
+y = W_down h -- two launches of libg4hip.so.  Weights are resident in HBM before
+timing starts; each step uses the next of several weight copies whose total
+exceeds twice the 256 MB Infinity Cache, so every step streams from HBM.
+Steps are captured in a HIP graph (one graph = one pass over the copies) and
+replayed; the timed region is bracketed by device synchronisation.
+
+Prints one JSON line.  `value` is GB/s of algorithmic bytes (each weight and
+activation byte counted once) per second; `roofline` covers the dominant
+kernel, timed with HIP events on the launch stream; `cpu_baseline` times the
+oracle's restatement of the reference's 512-bit Vector API path on the host
+cores over a bounded sample of the same workload.
+
+Other workloads: --workload q8_0_matvec | q4_0_ffn | q8_0_lm_head |
+q4_k_batched[:M] | moe[:T]; --all prints one line per workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gemma4.kt_amd"))
+
+import numpy as np  # noqa: E402
+
+METRIC = "quant matvec GB/s & % of HBM peak (Q8_0/Q4_0/Q4_K); MoE expert tokens/s"
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+Q8_0, Q4_0, Q4_K = 8, 2, 12
+
+
+def copies_for(nbytes: int, cap: int = 256) -> int:
+    """Weight copies so that one pass over them spans >= 2x the Infinity Cache."""
+    if nbytes >= 2 * MALL_BYTES:
+        return 1
+    return max(2, min(cap, math.ceil(2 * MALL_BYTES / nbytes)))
+
+
+class Workload:
+    """Device buffers + the per-step launch sequence of one workload."""
+
+    name = ""
+    unit = "GB/s"
+    step_bytes = 0          # algorithmic bytes per step
+    dominant_name = ""           # dominant kernel name (as rocprof reports it)
+    dominant_bytes = 0      # algorithmic bytes per launch of the dominant kernel
+    tokens_per_step = 0     # MoE: tokens per step
+    copies = 1
+
+    def step(self, i: int) -> None:
+        """Launch one step on weight copy / routing i (device work only, graph-capturable)."""
+        raise NotImplementedError
+
+    def dominant(self, i: int) -> None:
+        """Launch only the dominant kernel of step i (for its roofline timing)."""
+        self.step(i)
+
+    def cpu_step(self) -> None:
+        raise NotImplementedError
+
+    def config(self) -> dict:
+        raise NotImplementedError
+
+
+class FfnQ4_0(Workload):
+    name = "q4_0_ffn_decode_token"
+    dominant_name = "k_rows<FmtQ4_0, 32, EPI_GELU_PAIR> (gate+up fused)"
+
+    def __init__(self, g4, ctx, torch):
+        import synth
+        c = synth.q4_0_ffn()
+        self.c = c
+        dim, hidden = c["dim"], c["hidden"]
+        self.dim, self.hidden = dim, hidden
+        wbytes = c["gate"].nbytes + c["up"].nbytes + c["down"].nbytes
+        self.copies = copies_for(wbytes)
+        self.w = []
+        for _ in range(self.copies):
+            self.w.append(tuple(g4.FloatTensorFactory.create(ctx, Q4_0, c[k], n)
+                                for k, n in (("gate", hidden * dim), ("up", hidden * dim), ("down", dim * hidden))))
+        self.x = torch.from_numpy(c["x"]).cuda()
+        self.h = torch.empty(hidden, dtype=torch.float32, device="cuda")
+        self.y = torch.empty(dim, dtype=torch.float32, device="cuda")
+        # algorithmic bytes as quoted for this workload: the 3 weight matrices plus
+        # 122880 B of activations (x read by gate and up, gate/up written, h read, y written)
+        self.step_bytes = wbytes + 4 * (2 * dim + 2 * hidden + hidden + dim)
+        # fused gate+up launch: both matrices, x once, h written once
+        self.dominant_bytes = c["gate"].nbytes + c["up"].nbytes + 4 * dim + 4 * hidden
+        self.g4, self.ctx = g4, ctx
+
+    def step(self, i):
+        wg, wu, wd = self.w[i % self.copies]
+        self.g4.ffn_gate_up_dev(self.ctx, wg, wu, self.x, self.h, self.dim, self.hidden)
+        wd.matmul_dev(self.h, self.y, self.dim, self.hidden)
+
+    def dominant(self, i):
+        wg, wu, _ = self.w[i % self.copies]
+        self.g4.ffn_gate_up_dev(self.ctx, wg, wu, self.x, self.h, self.dim, self.hidden)
+
+    def cpu_setup(self, oracle):
+        self.oracle = oracle
+        self.gu_cat = np.concatenate([self.c["gate"], self.c["up"]])
+        self.ids = np.zeros((1, 1), np.int32)
+        self.one = np.ones((1, 1), np.float32)
+
+    def cpu_step(self):
+        self.oracle.moe(Q4_0, self.gu_cat, Q4_0, self.c["down"], self.c["x"].reshape(1, -1), self.ids, self.one,
+                        self.dim, self.hidden)
+
+    def config(self):
+        return {"workload": self.name, "format": "Q4_0", "gate_up": [self.hidden, self.dim],
+                "down": [self.dim, self.hidden], "algorithmic_bytes_per_step": self.step_bytes,
+                "weight_copies": self.copies}
+
+
+class MatvecQ8_0(Workload):
+    name = "q8_0_matvec_2048x2048"
+    dominant_name = "k_rows<FmtQ8_0, 32, EPI_STORE>"
+
+    def __init__(self, g4, ctx, torch):
+        import synth
+        c = synth.q8_0_matvec_2048()
+        self.c = c
+        self.copies = copies_for(c["w"].nbytes)
+        self.w = [g4.FloatTensorFactory.create(ctx, Q8_0, c["w"], 2048 * 2048) for _ in range(self.copies)]
+        self.x = torch.from_numpy(c["x"]).cuda()
+        self.y = torch.empty(2048, dtype=torch.float32, device="cuda")
+        self.step_bytes = c["w"].nbytes + 4 * 2048 * 2
+        self.dominant_bytes = self.step_bytes
+
+    def step(self, i):
+        self.w[i % self.copies].matmul_dev(self.x, self.y, 2048, 2048)
+
+    def cpu_setup(self, oracle):
+        self.oracle = oracle
+
+    def cpu_step(self):
+        self.oracle.matmul(Q8_0, self.c["w"], self.c["x"], 2048, 2048)
+
+    def config(self):
+        return {"workload": self.name, "format": "Q8_0", "w": [2048, 2048],
+                "algorithmic_bytes_per_step": self.step_bytes, "weight_copies": self.copies}
+
+
+class LmHeadQ8_0(Workload):
+    name = "q8_0_lm_head_262144x2048_argmax"
+    dominant_name = "k_rows<FmtQ8_0, 32, EPI_ARGMAX>"
+
+    def __init__(self, g4, ctx, torch):
+        import synth
+        c = synth.q8_0_lm_head()
+        self.c = c
+        V, D = c["dim0"], c["dim1"]
+        self.V, self.D = V, D
+        self.copies = copies_for(c["w"].nbytes)
+        self.w = [g4.FloatTensorFactory.create(ctx, Q8_0, c["w"], V * D) for _ in range(self.copies)]
+        self.x = torch.from_numpy(c["x"]).cuda()
+        self.logits = torch.empty(V, dtype=torch.float32, device="cuda")
+        self.idx = torch.zeros(1, dtype=torch.int32, device="cuda")
+        self.step_bytes = c["w"].nbytes + 4 * D + 4 * V + 4
+        self.dominant_bytes = self.step_bytes
+
+    def step(self, i):
+        self.w[i % self.copies].matmul_argmax_dev(self.x, self.logits, self.idx.data_ptr(), self.V, self.D)
+
+    def cpu_setup(self, oracle):
+        self.oracle = oracle
+
+    def cpu_step(self):
+        lg = self.oracle.matmul(Q8_0, self.c["w"], self.c["x"], self.V, self.D)
+        self.oracle.argmax(lg)
+
+    def cpu_sample_rows(self):
+        return 16384  # bounded CPU sample: a slice of the vocabulary rows
+
+    def cpu_step_rows(self, rows):
+        lg = self.oracle.matmul(Q8_0, self.c["w"], self.c["x"], rows, self.D)
+        self.oracle.argmax(lg)
+
+    def config(self):
+        return {"workload": self.name, "format": "Q8_0", "w": [self.V, self.D],
+                "algorithmic_bytes_per_step": self.step_bytes, "weight_copies": self.copies}
+
+
+class BatchedQ4_K(Workload):
+    dominant_name = "k_rows<FmtQ4_K, 32, EPI_STORE> (M segments)"
+
+    def __init__(self, g4, ctx, torch, m=8):
+        import synth
+        c = synth.q4_k_batched(m)
+        self.c, self.m = c, m
+        self.name = "q4_k_batched_8192x2048_m%d" % m
+        R, D = c["dim0"], c["dim1"]
+        self.R, self.D = R, D
+        self.copies = copies_for(c["w"].nbytes)
+        self.w = [g4.FloatTensorFactory.create(ctx, Q4_K, c["w"], R * D) for _ in range(self.copies)]
+        self.X = torch.from_numpy(np.ascontiguousarray(c["x"])).cuda()
+        self.Y = torch.empty((m, R), dtype=torch.float32, device="cuda")
+        self.step_bytes = c["w"].nbytes + 4 * m * (D + R)
+        self.dominant_bytes = self.step_bytes
+
+    def step(self, i):
+        self.w[i % self.copies].matmul_batch_dev(self.X, self.m, self.Y, self.R, self.D)
+
+    def cpu_setup(self, oracle):
+        self.oracle = oracle
+
+    def cpu_step(self):
+        for i in range(self.m):
+            self.oracle.matmul(Q4_K, self.c["w"], self.c["x"][i], self.R, self.D)
+
+    def config(self):
+        return {"workload": self.name, "format": "Q4_K", "w": [self.R, self.D], "m": self.m,
+                "algorithmic_bytes_per_step": self.step_bytes, "weight_copies": self.copies,
+                "flops_per_step": 2 * self.m * self.R * self.D}
+
+
+class MoeQ4_K(Workload):
+    unit = "tokens/s"
+    dominant_name = "k_rows<FmtQ4_K, 32, EPI_GELU_PAIR> (expert gate+up)"
+
+    def __init__(self, g4, ctx, torch, tokens=1, routings=32):
+        import synth
+        self.T = tokens
+        self.name = "moe_q4_k_128x(2816x2048+2048x1408)_top8_t%d" % tokens
+        base = synth.moe_q4_k(tokens)
+        E, D, FF, K = base["n_experts"], base["dim"], base["ff"], base["k"]
+        self.E, self.D, self.FF, self.K = E, D, FF, K
+        self.base = base
+        self.wgu = g4.FloatTensorFactory.create(ctx, Q4_K, base["gate_up"], E * 2 * FF * D)
+        self.wdn = g4.FloatTensorFactory.create(ctx, Q4_K, base["down"], E * D * FF)
+        self.copies = routings
+        self.logits, self.X, self.distinct = [], [], []
+        for r in range(routings):  # routing r = the logits/x streams of synth.moe_q4_k(tokens, routing_seed=r)
+            lg = synth.activations(synth.SEED_MOE_Q4_K, "router%d.%d" % (tokens, r), tokens * E).reshape(tokens, E)
+            x = synth.activations(synth.SEED_MOE_Q4_K, "x%d.%d" % (tokens, r), tokens * D).reshape(tokens, D)
+            ids, _ = g4.moe_route(ctx, lg, K, True)
+            self.distinct.append(len(np.unique(ids)))
+            self.logits.append(torch.from_numpy(lg).cuda())
+            self.X.append(torch.from_numpy(x).cuda())
+        self.ids = torch.zeros((tokens, K), dtype=torch.int32, device="cuda")
+        self.gw = torch.zeros((tokens, K), dtype=torch.float32, device="cuda")
+        self.Y = torch.empty((tokens, D), dtype=torch.float32, device="cuda")
+        per_expert = (2 * FF * D + D * FF) // 256 * 144
+        self.per_expert = per_expert
+        mean_distinct = float(np.mean(self.distinct))
+        self.step_bytes = int(mean_distinct * per_expert + 4 * tokens * (D + E + D))
+        self.dominant_bytes = int(mean_distinct * (2 * FF * D // 256 * 144))
+        self.tokens_per_step = tokens
+        self.g4, self.ctx = g4, ctx
+
+    def step(self, i):
+        r = i % self.copies
+        self.g4.moe_route_dev(self.ctx, self.logits[r], self.T, self.E, self.K, True, self.ids.data_ptr(), self.gw)
+        self.g4.moe_dev(self.ctx, self.wgu, self.wdn, self.X[r], self.T, self.D, self.FF, self.ids.data_ptr(),
+                        self.gw, self.K, self.Y)
+
+    def dominant(self, i):
+        # expert FFN launches of one routing (routing ids from the previous step's route)
+        r = i % self.copies
+        self.g4.moe_dev(self.ctx, self.wgu, self.wdn, self.X[r], self.T, self.D, self.FF, self.ids.data_ptr(),
+                        self.gw, self.K, self.Y)
+
+    def cpu_setup(self, oracle):
+        self.oracle = oracle
+        self.cpu_ids, self.cpu_w = oracle.route(self.base["logits"], self.K, True)
+
+    def cpu_step(self):
+        self.oracle.moe(Q4_K, self.base["gate_up"], Q4_K, self.base["down"], self.base["x"], self.cpu_ids,
+                        self.cpu_w, self.D, self.FF)
+
+    def config(self):
+        return {"workload": self.name, "format": "Q4_K", "experts": self.E, "top_k": self.K, "tokens": self.T,
+                "routings": self.copies, "mean_distinct_experts": float(np.mean(self.distinct)),
+                "algorithmic_bytes_per_step": self.step_bytes}
+
+
+def make_workload(spec: str, g4, ctx, torch) -> Workload:
+    name, _, arg = spec.partition(":")
+    if name == "q4_0_ffn":
+        return FfnQ4_0(g4, ctx, torch)
+    if name == "q8_0_matvec":
+        return MatvecQ8_0(g4, ctx, torch)
+    if name == "q8_0_lm_head":
+        return LmHeadQ8_0(g4, ctx, torch)
+    if name == "q4_k_batched":
+        return BatchedQ4_K(g4, ctx, torch, int(arg or 8))
+    if name == "moe":
+        return MoeQ4_K(g4, ctx, torch, int(arg or 1))
+    raise SystemExit("unknown workload %r" % spec)
+
+
+def cpu_baseline(wl: Workload, seconds: float) -> dict:
+    """Time the oracle (restated 512-bit Vector API path, OpenMP over rows like the
+    reference's ForkJoin pool) on the host cores over a bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    threads = oracle.nthreads()
+    wl.cpu_setup(oracle)
+    if isinstance(wl, LmHeadQ8_0):
+        rows = wl.cpu_sample_rows()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            wl.cpu_step_rows(rows)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= 1000:
+                break
+        frac = rows / wl.V
+        value = n * frac * wl.step_bytes / el / 1e9
+        sample = "%d passes over %d of %d vocabulary rows (%.1f s)" % (n, rows, wl.V, el)
+    else:
+        n, t0 = 0, time.perf_counter()
+        while True:
+            wl.cpu_step()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= 100000:
+                break
+        if wl.unit == "tokens/s":
+            value = n * wl.tokens_per_step / el
+        else:
+            value = n * wl.step_bytes / el / 1e9
+        sample = "%d steps of the same workload (%.1f s)" % (n, el)
+    return {"value": round(value, 3), "unit": wl.unit, "cores": threads, "kind": "port", "sample": sample}
+
+
+def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool) -> dict:
+    import torch
+    import g4hip as g4
+    if g4.device_count() == 0:
+        raise SystemExit("bench.py needs a HIP device")
+    torch.cuda.init()
+    ctx = g4.Context(0)
+    wl = make_workload(spec, g4, ctx, torch)
+    stream = torch.cuda.Stream()
+    copies = wl.copies
+    rounds = max(1, math.ceil(steps / copies))
+    steps = rounds * copies
+    dom_rounds = max(1, math.ceil(64 / copies))
+
+    def capture(fn):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            ctx.set_stream(stream.cuda_stream)
+            fn()
+        g.replay()
+        torch.cuda.synchronize()
+        return g
+
+    with torch.cuda.stream(stream):
+        ctx.set_stream(stream.cuda_stream)
+        for i in range(warmup):
+            wl.step(i)
+        torch.cuda.synchronize()
+        step_graph = dom_graph = None
+        if use_graph:
+            try:
+                step_graph = capture(lambda: [wl.step(i) for i in range(copies)])
+                dom_graph = capture(lambda: [wl.dominant(i) for i in range(copies)])
+            except Exception as e:
+                print("graph capture unavailable (%s); timing eager launches" % str(e).splitlines()[0],
+                      file=sys.stderr)
+                step_graph = dom_graph = None
+                torch.cuda.synchronize()
+        ctx.set_stream(stream.cuda_stream)
+        # timed region: `steps` steps, device-synchronised on both sides
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(rounds):
+            if step_graph is not None:
+                step_graph.replay()
+            else:
+                for i in range(copies):
+                    wl.step(i)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        # dominant kernel: HIP events on the launch stream around back-to-back launches
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for _ in range(dom_rounds):
+            if dom_graph is not None:
+                dom_graph.replay()
+            else:
+                for i in range(copies):
+                    wl.dominant(i)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        launches = dom_rounds * copies
+        kern_ms = ev0.elapsed_time(ev1) / launches
+        ctx.set_stream(None)
+    ms_per_step = elapsed * 1e3 / steps
+    if wl.unit == "tokens/s":
+        value = wl.tokens_per_step / (ms_per_step / 1e3)
+        gbs_step = wl.step_bytes / (ms_per_step / 1e3) / 1e9
+    else:
+        value = wl.step_bytes / (ms_per_step / 1e3) / 1e9
+        gbs_step = value
+    achieved = wl.dominant_bytes / (kern_ms / 1e3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": wl.unit,
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded GGUF blocks and activations (gemma4.kt_amd/synth.py)",
+        "config": dict(wl.config(), graph=step_graph is not None, step_gbs=round(gbs_step, 2),
+                       hbm_fraction=round(gbs_step / HBM_PEAK_GBS, 4)),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": wl.dominant_name, "bytes_per_launch": wl.dominant_bytes,
+                     "avg_launch_us": round(kern_ms * 1e3, 3), "launches_timed": launches},
+    }
+    if cpu_seconds > 0:
+        line["cpu_baseline"] = cpu_baseline(wl, cpu_seconds)
+    ctx.close()
+    return line
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--workload", default="q4_0_ffn")
+    ap.add_argument("--all", action="store_true", help="one JSON line per workload")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (0 = skip)")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each box has one MI355X); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    specs = [args.workload]
+    if args.all:
+        specs = ["q4_0_ffn", "q8_0_matvec", "q8_0_lm_head", "q4_k_batched:1", "q4_k_batched:8",
+                 "q4_k_batched:32", "q4_k_batched:64", "moe:1", "moe:16"]
+    for s in specs:
+        line = run(s, args.steps, args.warmup, args.cpu_seconds, not args.eager)
+        print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

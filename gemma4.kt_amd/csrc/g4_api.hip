@@ -22,9 +22,8 @@ struct g4_ctx {
   g4::DevInfo dev;
   char *scratch;  // grow-only device buffer for staging and intermediates
   size_t scratch_bytes;
-  float *am_val;  // argmax partials, counter (kept at zero between launches) and result
+  float *am_val;  // per-block argmax partials and a result slot
   int32_t *am_idx;
-  uint32_t *am_counter;
   int32_t *am_out;
 };
 
@@ -217,30 +216,36 @@ int argmax_rows_dev(g4_ctx *ctx, const g4_weight *w, int64_t off, const float *d
   g4::RowsArgs a = plain_rows(w, off, d_x, d_logits, dim0, dim1);
   a.am_val = ctx->am_val;
   a.am_idx = ctx->am_idx;
-  a.am_counter = ctx->am_counter;
   a.am_out = d_index;
   return launch_status(g4::launch_rows(w->type, g4::EPI_ARGMAX, a, 1, ctx->dev, nullptr, ctx->stream),
                        "matmul_argmax");
 }
 
-int ffn_dev(g4_ctx *ctx, const g4_weight *wg, const g4_weight *wu, const g4_weight *wd, const float *d_x,
-            float *d_y, float *d_h, float *d_gu, int32_t dim, int32_t hidden) {
+// h = gelu(W_gate x) * (W_up x): one paired launch (d_gu: 2*hidden floats, used by the generic path only).
+int gate_up_dev(g4_ctx *ctx, const g4_weight *wg, const g4_weight *wu, const float *d_x, float *d_h, float *d_gu,
+                int32_t dim, int32_t hidden) {
   g4::RowsArgs a = plain_rows(wg, 0, d_x, d_h, hidden, dim);
   a.W1 = wu->d;
-  G4_TRY(launch_status(g4::launch_rows(wg->type, g4::EPI_GELU_PAIR, a, 1, ctx->dev, d_gu, ctx->stream), "ffn"));
+  return launch_status(g4::launch_rows(wg->type, g4::EPI_GELU_PAIR, a, 1, ctx->dev, d_gu, ctx->stream), "ffn");
+}
+
+int ffn_dev(g4_ctx *ctx, const g4_weight *wg, const g4_weight *wu, const g4_weight *wd, const float *d_x,
+            float *d_y, float *d_h, float *d_gu, int32_t dim, int32_t hidden) {
+  G4_TRY(gate_up_dev(ctx, wg, wu, d_x, d_h, d_gu, dim, hidden));
   g4::RowsArgs b = plain_rows(wd, 0, d_h, d_y, dim, hidden);
   return launch_status(g4::launch_rows(wd->type, g4::EPI_STORE, b, 1, ctx->dev, nullptr, ctx->stream), "ffn");
 }
 
+// w_down may be null (gate/up half only).
 int check_ffn(g4_ctx *ctx, const g4_weight *wg, const g4_weight *wu, const g4_weight *wd, int32_t dim,
               int32_t hidden) {
   G4_TRY(check_weight(ctx, wg, "w_gate"));
   G4_TRY(check_weight(ctx, wu, "w_up"));
-  G4_TRY(check_weight(ctx, wd, "w_down"));
+  if (wd) G4_TRY(check_weight(ctx, wd, "w_down"));
   if (dim <= 0 || hidden <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "ffn dims must be positive (%d, %d)", dim, hidden);
   G4_TRY(check_rows(wg, 0, hidden, dim));
   G4_TRY(check_rows(wu, 0, hidden, dim));
-  G4_TRY(check_rows(wd, 0, dim, hidden));
+  if (wd) G4_TRY(check_rows(wd, 0, dim, hidden));
   if (wg->type != wu->type) return fail(G4_ERR_UNSUPPORTED, "ffn: gate and up weights must share one GGML type");
   return G4_OK;
 }
@@ -390,7 +395,7 @@ int g4_open(int ordinal, g4_ctx **out) {
   c->stream = c->own_stream;
   const int nb = g4::max_argmax_blocks(c->dev);
   void *p = nullptr;
-  size_t bytes = up(sizeof(float) * nb) + up(sizeof(int32_t) * nb) + up(sizeof(uint32_t)) + up(sizeof(int32_t));
+  size_t bytes = up(sizeof(float) * nb) + up(sizeof(int32_t) * nb) + up(sizeof(int32_t));
   e = hipMalloc(&p, bytes);
   if (e != hipSuccess) {
     (void)hipStreamDestroy(c->own_stream);
@@ -400,8 +405,7 @@ int g4_open(int ordinal, g4_ctx **out) {
   char *b = (char *)p;
   c->am_val = (float *)b;
   c->am_idx = (int32_t *)(b + up(sizeof(float) * nb));
-  c->am_counter = (uint32_t *)(b + up(sizeof(float) * nb) + up(sizeof(int32_t) * nb));
-  c->am_out = (int32_t *)((char *)c->am_counter + up(sizeof(uint32_t)));
+  c->am_out = (int32_t *)(b + up(sizeof(float) * nb) + up(sizeof(int32_t) * nb));
   e = hipMemset(p, 0, bytes);
   if (e != hipSuccess) {
     (void)hipFree(p);
@@ -587,7 +591,7 @@ int g4_matmul_argmax(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const
   G4_TRY(copy_in(ctx, dx, that, sizeof(float) * (size_t)dim1));
   if (dim1 == 0) {
     G4_HIP(hipMemsetAsync(dy, 0, sizeof(float) * (size_t)dim0, ctx->stream), "hipMemsetAsync");
-    G4_TRY(launch_status(g4::launch_argmax(dy, dim0, ctx->am_val, ctx->am_idx, ctx->am_counter, di, ctx->dev,
+    G4_TRY(launch_status(g4::launch_argmax(dy, dim0, ctx->am_val, ctx->am_idx, di, ctx->dev,
                                            ctx->stream), "argmax"));
   } else {
     G4_TRY(argmax_rows_dev(ctx, w, this_offset, dx, dy, di, dim0, dim1));
@@ -614,7 +618,7 @@ int g4_matmul_argmax_dev(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, c
   }
   if (dim1 == 0) {
     G4_HIP(hipMemsetAsync(dy, 0, sizeof(float) * (size_t)dim0, ctx->stream), "hipMemsetAsync");
-    return launch_status(g4::launch_argmax(dy, dim0, ctx->am_val, ctx->am_idx, ctx->am_counter, d_index, ctx->dev,
+    return launch_status(g4::launch_argmax(dy, dim0, ctx->am_val, ctx->am_idx, d_index, ctx->dev,
                                            ctx->stream), "argmax");
   }
   return argmax_rows_dev(ctx, w, this_offset, d_that, dy, d_index, dim0, dim1);
@@ -632,7 +636,7 @@ int g4_argmax(g4_ctx *ctx, const float *v, int32_t n, int32_t *index) {
   int32_t *di = (int32_t *)(ctx->scratch + oi);
   G4_TRY(copy_in(ctx, dv, v, sizeof(float) * (size_t)n));
   G4_TRY(launch_status(
-      g4::launch_argmax(dv, n, ctx->am_val, ctx->am_idx, ctx->am_counter, di, ctx->dev, ctx->stream), "argmax"));
+      g4::launch_argmax(dv, n, ctx->am_val, ctx->am_idx, di, ctx->dev, ctx->stream), "argmax"));
   G4_TRY(copy_out(ctx, index, di, sizeof(int32_t)));
   return finish(ctx);
 }
@@ -643,7 +647,7 @@ int g4_argmax_dev(g4_ctx *ctx, const float *d_v, int32_t n, int32_t *d_index) {
   if (!d_v || !d_index) return fail(G4_ERR_INVALID_ARGUMENT, "v/index is null");
   G4_TRY(use_device(ctx));
   return launch_status(
-      g4::launch_argmax(d_v, n, ctx->am_val, ctx->am_idx, ctx->am_counter, d_index, ctx->dev, ctx->stream), "argmax");
+      g4::launch_argmax(d_v, n, ctx->am_val, ctx->am_idx, d_index, ctx->dev, ctx->stream), "argmax");
 }
 
 // ------------------------------------------------------------- dequant ----
@@ -711,6 +715,41 @@ int g4_ffn_dev(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, cons
   G4_TRY(ensure_scratch(ctx, c.off));
   float *dh = (float *)(ctx->scratch + oh), *dg = (float *)(ctx->scratch + og);
   return ffn_dev(ctx, w_gate, w_up, w_down, d_x, d_y, dh, dg, dim, hidden);
+}
+
+int g4_ffn_gate_up(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const float *x, float *h,
+                   int32_t dim, int32_t hidden) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_ffn(ctx, w_gate, w_up, nullptr, dim, hidden));
+  if (!x || !h) return fail(G4_ERR_INVALID_ARGUMENT, "x/h is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t ox = c.add(sizeof(float) * (size_t)dim), oh = c.add(sizeof(float) * (size_t)hidden),
+         og = c.add(sizeof(float) * 2 * (size_t)hidden);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  float *dx = (float *)(ctx->scratch + ox), *dh = (float *)(ctx->scratch + oh), *dg = (float *)(ctx->scratch + og);
+  G4_TRY(copy_in(ctx, dx, x, sizeof(float) * (size_t)dim));
+  G4_TRY(gate_up_dev(ctx, w_gate, w_up, dx, dh, dg, dim, hidden));
+  G4_TRY(copy_out(ctx, h, dh, sizeof(float) * (size_t)hidden));
+  return finish(ctx);
+}
+
+int g4_ffn_gate_up_dev(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const float *d_x, float *d_h,
+                       int32_t dim, int32_t hidden) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_ffn(ctx, w_gate, w_up, nullptr, dim, hidden));
+  if (!d_x || !d_h) return fail(G4_ERR_INVALID_ARGUMENT, "x/h is null");
+  G4_TRY(use_device(ctx));
+  float *dg = nullptr;
+  g4::RowsArgs a = plain_rows(w_gate, 0, d_x, d_h, hidden, dim);
+  a.W1 = w_up->d;
+  if (!g4::rows_fast_ok(w_gate->type, a, true)) {
+    Carve c;
+    size_t og = c.add(sizeof(float) * 2 * (size_t)hidden);
+    G4_TRY(ensure_scratch(ctx, c.off));
+    dg = (float *)(ctx->scratch + og);
+  }
+  return gate_up_dev(ctx, w_gate, w_up, d_x, d_h, dg, dim, hidden);
 }
 
 // ------------------------------------------------------------------ moe ----

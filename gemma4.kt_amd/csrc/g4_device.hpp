@@ -115,7 +115,7 @@ G4_DEV float dot_elem(const uint8_t *W, int64_t idx, int j, int dim1) {
 
 // Q8_0: {fp16 d, int8 q[32]} x 2 = 17 dwords starting dword-aligned (68 * k).
 struct FmtQ8_0 {
-  static constexpr int TYPE = T_Q8_0, NDW = 17, NS = 0, RT = 4;
+  static constexpr int TYPE = T_Q8_0, NDW = 17, NS = 0, RT = 2;
   G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
     const uint8_t *p = W + (e >> 6) * 68;
     const u32x4a4 *v = (const u32x4a4 *)p;
@@ -287,7 +287,7 @@ struct FmtHalf {
 
 // F32: 64 floats = 16 dwordx4.
 struct FmtF32 {
-  static constexpr int TYPE = T_F32, NDW = 64, NS = 0, RT = 2;
+  static constexpr int TYPE = T_F32, NDW = 64, NS = 0, RT = 1;
   G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
     const u32x4 *v = (const u32x4 *)(W + e * 4);
 #pragma unroll
@@ -313,6 +313,63 @@ struct FmtF32 {
 // Wave reductions.
 // ---------------------------------------------------------------------------
 
+// Partner value for the butterfly step S <= 8 inside a 16-lane row, by DPP:
+// S=8 row_ror:8 (lane ^ 8), S=4 row_half_mirror (7 - i within 8 lanes, which
+// flips bit 2), S=2 quad_perm [2,3,0,1], S=1 quad_perm [1,0,3,2].  Each is an
+// involution whose partner differs in bit S, which is all the butterfly needs.
+template <int S>
+G4_DEV float dpp_partner(float v) {
+  static_assert(S == 8 || S == 4 || S == 2 || S == 1, "row-local step");
+  constexpr int ctrl = S == 8 ? 0x128 : S == 4 ? 0x141 : S == 2 ? 0x4E : 0xB1;
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+}
+
+// One transposing butterfly step at distance S: lanes with bit S clear return
+// A(self) + A(partner), lanes with bit S set return B(self) + B(partner).
+// S = 32 / 16 use the gfx950 permlane swaps (one instruction moves both halves).
+template <int S>
+G4_DEV float tstep(float A, float B, int lane) {
+  if constexpr (S == 32) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(A), __float_as_uint(B), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if constexpr (S == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(A), __float_as_uint(B), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    const bool upper = (lane & S) != 0;
+    const float send = upper ? A : B, keep = upper ? B : A;
+    return keep + dpp_partner<S>(send);
+  }
+}
+
+// Plain butterfly step at distance S: every lane gets v(self) + v(partner).
+template <int S>
+G4_DEV float pstep(float v) {
+  if constexpr (S == 32) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if constexpr (S == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    return v + dpp_partner<S>(v);
+  }
+}
+
+template <int S, int N, int NV>
+G4_DEV void reduce_steps(float (&v)[NV], int lane) {
+  if constexpr (S >= 1) {
+    if constexpr (N > 1) {
+#pragma unroll
+      for (int j = 0; j < N / 2; ++j) v[j] = tstep<S>(v[j], v[j + N / 2], lane);
+      reduce_steps<S / 2, N / 2>(v, lane);
+    } else {
+      v[0] = pstep<S>(v[0]);
+      reduce_steps<S / 2, 1>(v, lane);
+    }
+  }
+}
+
 // Sum N values over the LPR lanes of each lane group (LPR a power of two, N <= LPR).
 // The first log2(N) butterfly steps exchange half of the remaining values
 // (a transposing reduction), the rest reduce one value.  On return, lane q of a
@@ -320,25 +377,7 @@ struct FmtF32 {
 template <int N, int LPR>
 G4_DEV float reduce_transpose(float (&v)[N], int lane) {
   static_assert((N & (N - 1)) == 0 && (LPR & (LPR - 1)) == 0 && N <= LPR, "powers of two");
-  int n = N;
-#pragma unroll
-  for (int s = LPR / 2; s >= 1; s >>= 1) {
-    if (n > 1) {
-      const bool upper = (lane & s) != 0;
-      const int h = n / 2;
-#pragma unroll
-      for (int j = 0; j < N / 2; ++j) {
-        if (j < h) {
-          float send = upper ? v[j] : v[j + h];
-          float keep = upper ? v[j + h] : v[j];
-          v[j] = keep + __shfl_xor(send, s, 64);
-        }
-      }
-      n = h;
-    } else {
-      v[0] += __shfl_xor(v[0], s, 64);
-    }
-  }
+  reduce_steps<LPR / 2, N>(v, lane);
   return v[0];
 }
 
@@ -355,14 +394,43 @@ G4_DEV float wave_sum(float v) {
 G4_DEV bool am_better(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
 G4_DEV float am_key(float v, int64_t idx) { return v != v ? (idx == 0 ? __builtin_inff() : -__builtin_inff()) : v; }
 
-G4_DEV void am_wave(float &v, int &i) {
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) {
-    float ov = __shfl_xor(v, s, 64);
-    int oi = __shfl_xor(i, s, 64);
-    if (am_better(ov, oi, v, i)) v = ov, i = oi;
+// Value of the butterfly partner at distance S (lane ^ S for S >= 16 and S = 8,
+// 2, 1; the half-row mirror for S = 4), without going through LDS.
+template <int S>
+G4_DEV uint32_t partner_u32(uint32_t v, int lane) {
+  if constexpr (S == 32) {
+    auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);  // r[0] = low half, r[1] = high half
+    return (lane & 32) ? r[0] : r[1];
+  } else if constexpr (S == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);  // r[0] = even rows, r[1] = odd rows
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    constexpr int ctrl = S == 8 ? 0x128 : S == 4 ? 0x141 : S == 2 ? 0x4E : 0xB1;
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctrl, 0xF, 0xF, false);
   }
 }
+
+template <int S>
+G4_DEV void am_step(float &v, int &i, int lane) {
+  const float ov = __uint_as_float(partner_u32<S>(__float_as_uint(v), lane));
+  const int oi = (int)partner_u32<S>((uint32_t)i, lane);
+  if (am_better(ov, oi, v, i)) v = ov, i = oi;
+}
+
+// (value, index) arg-max over the 64 lanes of a wave; every lane ends with the result.
+G4_DEV void am_wave(float &v, int &i) {
+  const int lane = __lane_id();
+  am_step<32>(v, i, lane);
+  am_step<16>(v, i, lane);
+  am_step<8>(v, i, lane);
+  am_step<4>(v, i, lane);
+  am_step<2>(v, i, lane);
+  am_step<1>(v, i, lane);
+}
+
+// Coherent (L2) load that does not serialise like a volatile access.
+G4_DEV float load_agent(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+G4_DEV int load_agent(const int32_t *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 // Llama.kt:23-25 gelu, evaluated in double like the reference.
 G4_DEV float gelu_ref(float xf) {

@@ -29,10 +29,9 @@ struct RowsArgs {
   int32_t x_div;
   float *y;
   int64_t y_stride;
-  // EPI_ARGMAX: per-block partials, arrival counter (zero between launches), result
+  // EPI_ARGMAX: per-block partials (max_argmax_blocks() slots) and the result index
   float *am_val;
   int32_t *am_idx;
-  uint32_t *am_counter;
   int32_t *am_out;
 };
 
@@ -47,14 +46,15 @@ bool rows_fast_ok(int type, const RowsArgs &a, bool paired);
 // Launch the matvec engine over `segments` segments.  For EPI_GELU_PAIR the
 // launch writes h[r] = gelu(W0 row r . x) * (W1 row r . x); on the generic path
 // that needs `scratch` of 2 * rows * segments floats.  For EPI_ARGMAX, segments
-// must be 1 and am_* point to at least max_argmax_blocks() partials.
+// must be 1 and am_val/am_idx hold max_argmax_blocks() partials (a second, one-block
+// launch reduces them into *am_out).
 hipError_t launch_rows(int type, int epi, const RowsArgs &a, int segments, const DevInfo &dev, float *scratch,
                        hipStream_t stream);
 int max_argmax_blocks(const DevInfo &dev);
 
 hipError_t launch_dequant(int type, const uint8_t *W, int64_t offset, int64_t n, float *out, hipStream_t stream);
-hipError_t launch_argmax(const float *v, int32_t n, float *part_val, int32_t *part_idx, uint32_t *counter,
-                         int32_t *out, const DevInfo &dev, hipStream_t stream);
+hipError_t launch_argmax(const float *v, int32_t n, float *part_val, int32_t *part_idx, int32_t *out,
+                         const DevInfo &dev, hipStream_t stream);
 hipError_t launch_route(const float *logits, int32_t T, int32_t n_experts, int32_t k, int32_t renorm,
                         const float *expert_scale, int32_t *ids, float *weights, hipStream_t stream);
 hipError_t launch_moe_combine(const float *ys, const float *weights, int32_t T, int32_t k, int32_t dim, float *Y,

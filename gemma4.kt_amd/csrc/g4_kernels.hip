@@ -18,22 +18,58 @@
 
 namespace g4 {
 
+// ------------------------------------------------------------ arg-max ----
+// Cross-block (value, index) reduction in two launches.  Inside one launch a
+// block-to-block handoff needs device-scope release/acquire fences, which on a
+// multi-XCD part write back / invalidate the per-XCD L2 (the L2s do not snoop
+// each other): measured at tens of microseconds for a few hundred blocks behind
+// 1 MB of freshly written logits.  So each block stores its partial with a plain
+// store and k_argmax_final (one block) reduces them after the kernel boundary.
+
+// (value, index) of the block in thread 0 (all threads call, uniform control flow).
+__device__ void am_block(float &v, int &i) {
+  __shared__ float rv[4];
+  __shared__ int ri[4];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, wpb = blockDim.x >> 6;
+  am_wave(v, i);
+  __syncthreads();
+  if (lane == 0) rv[wid] = v, ri[wid] = i;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int w = 1; w < wpb; ++w)
+      if (am_better(rv[w], ri[w], v, i)) v = rv[w], i = ri[w];
+}
+
+__device__ void am_partial(float v, int i, float *pv, int32_t *pi) {
+  am_block(v, i);
+  if (threadIdx.x == 0) pv[blockIdx.x] = v, pi[blockIdx.x] = i;
+}
+
+// One 256-thread block: best of n block partials -> *out.
+__global__ __launch_bounds__(256) void k_argmax_final(const float *pv, const int32_t *pi, int n, int32_t *out) {
+  float v = -__builtin_inff();
+  int i = INT_MAX;
+  for (int b = threadIdx.x; b < n; b += 256)
+    if (am_better(pv[b], pi[b], v, i)) v = pv[b], i = pi[b];
+  am_block(v, i);
+  if (threadIdx.x == 0) *out = i;
+}
+
 // --------------------------------------------------------------- engine ----
 
-template <class F, int LPR, int EPI>
+template <class F, int LPR, int CPL, int EPI, bool MULTI>
 __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
-  constexpr int RT = F::RT;
+  constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1;  // row steps per tile (about F::RT chunk loads per lane)
   constexpr int RPW = 64 / LPR;                  // rows in flight per step (one per lane group)
   constexpr int TR = RT * RPW;                   // physical rows per tile
   constexpr int LRT = (EPI == EPI_GELU_PAIR) ? TR / 2 : TR;  // logical rows per tile
-  constexpr int PX = LPR * 64;                   // columns per pass
-  static_assert(EPI != EPI_GELU_PAIR || RT >= 2, "paired tiles need two steps");
+  constexpr int NDW = F::NDW;
+  static_assert(RT >= 1, "tile");
+  static_assert(EPI != EPI_GELU_PAIR || (RT >= 2 && CPL == 1), "paired tiles: gate and up steps, one pass");
 
-  __shared__ float4 xl[PX / 4];
-  __shared__ float red_v[4];
-  __shared__ int red_i[4];
-
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: tile loop control stays scalar
+  const int wpb = blockDim.x >> 6;
   const int gi = lane / LPR, q = lane % LPR;
   const int seg = blockIdx.y;
   const int expert = a.ids ? a.ids[seg] : 0;
@@ -43,141 +79,138 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   float *y = a.y ? a.y + (int64_t)seg * a.y_stride : nullptr;
 
   const int n_tiles = (a.rows + LRT - 1) / LRT;
-  const int nwv = gridDim.x * 4, wv = blockIdx.x * 4 + wid;
+  const int nwv = gridDim.x * wpb, wv = blockIdx.x * wpb + wid;
   const int tpw = (n_tiles + nwv - 1) / nwv;
-  const int t0 = wv * tpw, t1 = min(n_tiles, t0 + tpw);
+  const int t0 = min(n_tiles, wv * tpw), t1 = min(n_tiles, t0 + tpw);
   const int C = a.dim1 >> 6;
-  const int passes = (C + LPR - 1) / LPR;
+  const int passes = MULTI ? (C + LPR * CPL - 1) / (LPR * CPL) : 1;
+
+  // row (logical index, matrix, base) of tile t, step k for this lane's group
+  auto row_of = [&](int t, int k, int &lr, const uint8_t *&W, int64_t &base) {
+    if constexpr (EPI == EPI_GELU_PAIR) {
+      lr = t * LRT + (k % (RT / 2)) * RPW + gi;
+      W = k < RT / 2 ? a.W0 : a.W1;
+      base = k < RT / 2 ? a.base0 : a.base1;
+    } else {
+      lr = t * LRT + k * RPW + gi;
+      W = a.W0;
+      base = a.base0;
+    }
+  };
+
+  // `live` false: a prefetch past the wave's last tile (issued anyway so every
+  // path through the loop has the same number of loads in flight).
+  auto load_tile = [&](int t, int pass, bool live, uint32_t (&D)[RT][CPL][NDW], bool (&ok)[RT][CPL],
+                       int64_t (&E)[RT][CPL]) {
+#pragma unroll
+    for (int k = 0; k < RT; ++k) {
+      int lr;
+      const uint8_t *W;
+      int64_t base;
+      row_of(t, k, lr, W, base);
+#pragma unroll
+      for (int u = 0; u < CPL; ++u) {
+        const int c = (pass * CPL + u) * LPR + q;
+        ok[k][u] = live && c < C && lr < a.rows && !bad_expert;
+        E[k][u] = base + ebase + (int64_t)lr * a.row_stride + (int64_t)c * 64;
+        // Unconditional load (lanes past the row or the tile read the tensor's first
+        // chunk, always in bounds, and their result is masked): no branch around a
+        // load, so the compiler can count outstanding loads and wait for this tile only.
+        F::load(W, ok[k][u] ? E[k][u] : 0, D[k][u]);
+      }
+    }
+  };
 
   float best_v = -__builtin_inff();
   int best_i = INT_MAX;
 
-  for (int pass = 0; pass < passes; ++pass) {
-    __syncthreads();
-    for (int f4 = tid; f4 < PX / 4; f4 += 256) {
-      const int col = pass * PX + f4 * 4;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (col < a.dim1) v = make_float4(x[col], x[col + 1], x[col + 2], x[col + 3]);
-      const int qq = f4 >> 4, i = f4 & 15;
-      xl[qq * 16 + (i ^ (qq & 15))] = v;
-    }
-    __syncthreads();
-
-    float xv[64];
+  auto finish_tile = [&](int t, int pass, const uint32_t (&D)[RT][CPL][NDW], const bool (&ok)[RT][CPL],
+                         const int64_t (&E)[RT][CPL], const float (&xv)[CPL][64], const float (&xs)[CPL][F::NS > 0 ? F::NS : 1]) {
+    float v[RT];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float4 t = xl[q * 16 + (i ^ (q & 15))];
-      xv[4 * i] = t.x; xv[4 * i + 1] = t.y; xv[4 * i + 2] = t.z; xv[4 * i + 3] = t.w;
-    }
-    float xs[F::NS > 0 ? F::NS : 1];
-    F::sums(xv, xs);
-
-    const int c = pass * LPR + q;
-    const bool active = c < C;
-    const int64_t ecol = (int64_t)c * 64;
-    const bool last_pass = pass == passes - 1;
-
-    for (int t = t0; t < t1; ++t) {
-      uint32_t D[RT][F::NDW];
-      int64_t E[RT];
-      bool ok[RT];
+    for (int k = 0; k < RT; ++k) {
+      float acc = 0.f;
 #pragma unroll
-      for (int k = 0; k < RT; ++k) {
-        int lr;
-        const uint8_t *W;
-        int64_t base;
-        if constexpr (EPI == EPI_GELU_PAIR) {
-          lr = t * LRT + (k % (RT / 2)) * RPW + gi;
-          W = k < RT / 2 ? a.W0 : a.W1;
-          base = k < RT / 2 ? a.base0 : a.base1;
-        } else {
-          lr = t * LRT + k * RPW + gi;
-          W = a.W0;
-          base = a.base0;
-        }
-        ok[k] = active && lr < a.rows && !bad_expert;
-        E[k] = base + ebase + (int64_t)lr * a.row_stride + ecol;
-        if (ok[k]) {
-          F::load(W, E[k], D[k]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < F::NDW; ++i) D[k][i] = 0u;
-        }
+      for (int u = 0; u < CPL; ++u) {
+        const float r = F::dot(D[k][u], xv[u], xs[u], E[k][u]);
+        acc += ok[k][u] ? r : 0.f;
       }
-      float v[RT];
-#pragma unroll
-      for (int k = 0; k < RT; ++k) {
-        float r = F::dot(D[k], xv, xs, E[k]);
-        v[k] = ok[k] ? r : 0.f;
-      }
-      const float r = reduce_transpose<RT, LPR>(v, lane);
-      const int k = q / (LPR / RT);
-      const bool writer = (q % (LPR / RT)) == 0;
-
-      if constexpr (EPI == EPI_GELU_PAIR) {
-        const float up = __shfl_xor(r, LPR / 2, 64);
-        const int lr = t * LRT + (k % (RT / 2)) * RPW + gi;
-        if (writer && k < RT / 2 && lr < a.rows) y[lr] = gelu_ref(r) * up;
-      } else {
-        const int lr = t * LRT + k * RPW + gi;
-        if (writer && lr < a.rows) {
-          float val = r;
-          if (y) {
+      v[k] = acc;
+    }
+    const float r = reduce_transpose<RT, LPR>(v, lane);
+    const int k = q / (LPR / RT);
+    const bool writer = (q % (LPR / RT)) == 0;
+    if constexpr (EPI == EPI_GELU_PAIR) {
+      const float up = __shfl_xor(r, LPR / 2, 64);
+      const int lr = t * LRT + (k % (RT / 2)) * RPW + gi;
+      if (writer && k < RT / 2 && lr < a.rows) y[lr] = gelu_ref(r) * up;
+    } else {
+      const int lr = t * LRT + k * RPW + gi;
+      if (writer && lr < a.rows) {
+        float val = r;
+        if (y) {
+          // only the multi-pass kernels read back (a load here would make every
+          // single-pass tile wait for the prefetched one: vmcnt retires in order)
+          if constexpr (MULTI) {
             if (pass > 0) val += y[lr];
-            y[lr] = val;
           }
-          if constexpr (EPI == EPI_ARGMAX) {
-            if (last_pass) {
-              const float key = am_key(val, lr);
-              if (am_better(key, lr, best_v, best_i)) best_v = key, best_i = lr;
-            }
+          y[lr] = val;
+        }
+        if constexpr (EPI == EPI_ARGMAX) {
+          if (!MULTI || pass == passes - 1) {
+            const float key = am_key(val, lr);
+            if (am_better(key, lr, best_v, best_i)) best_v = key, best_i = lr;
           }
         }
       }
     }
+  };
+
+  for (int pass = 0; pass < passes; ++pass) {
+    uint32_t DA[RT][CPL][NDW], DB[RT][CPL][NDW];
+    bool okA[RT][CPL], okB[RT][CPL];
+    int64_t EA[RT][CPL], EB[RT][CPL];
+    // This lane's x columns first, straight from global memory (x is small and
+    // L2-resident after the first wave touches it); the weight loads go out
+    // right after, so the wait for x (vmcnt retires in issue order) never
+    // covers the weight latency, and no workgroup barrier is needed.
+    float xv[CPL][64];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+      const int c = (pass * CPL + u) * LPR + q;
+      const bool in = c < C;
+      // dword alignment is all a caller's x guarantees; gfx950 takes 128-bit loads at that alignment
+      const u32x4a4 *xp = (const u32x4a4 *)(x + (int64_t)(in ? c : 0) * 64);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const u32x4a4 t = xp[i];
+        xv[u][4 * i] = in ? __uint_as_float(t.x) : 0.f;
+        xv[u][4 * i + 1] = in ? __uint_as_float(t.y) : 0.f;
+        xv[u][4 * i + 2] = in ? __uint_as_float(t.z) : 0.f;
+        xv[u][4 * i + 3] = in ? __uint_as_float(t.w) : 0.f;
+      }
+    }
+    load_tile(t0, pass, t0 < t1, DA, okA, EA);
+    float xs[CPL][F::NS > 0 ? F::NS : 1];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) F::sums(xv[u], xs[u]);
+
+    // software pipeline: tile t+1 is in flight while tile t is unpacked and
+    // reduced.  The scheduling barriers keep the compiler from sinking the next
+    // tile's loads into the current tile's arithmetic.
+    for (int t = t0; t < t1; t += 2) {
+      load_tile(t + 1, pass, t + 1 < t1, DB, okB, EB);
+      __builtin_amdgcn_sched_barrier(0);
+      finish_tile(t, pass, DA, okA, EA, xv, xs);
+      __builtin_amdgcn_sched_barrier(0);
+      load_tile(t + 2, pass, t + 2 < t1, DA, okA, EA);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 1 < t1) finish_tile(t + 1, pass, DB, okB, EB, xv, xs);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
-  if constexpr (EPI == EPI_ARGMAX) {
-    am_wave(best_v, best_i);
-    if (lane == 0) red_v[wid] = best_v, red_i[wid] = best_i;
-    __syncthreads();
-    __shared__ bool is_last;
-    if (tid == 0) {
-      float bv = red_v[0];
-      int bi = red_i[0];
-      for (int w = 1; w < 4; ++w)
-        if (am_better(red_v[w], red_i[w], bv, bi)) bv = red_v[w], bi = red_i[w];
-      a.am_val[blockIdx.x] = bv;
-      a.am_idx[blockIdx.x] = bi;
-      __threadfence();
-      const uint32_t prev = atomicAdd(a.am_counter, 1u);
-      is_last = prev == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (is_last) {
-      __threadfence();
-      float bv = -__builtin_inff();
-      int bi = INT_MAX;
-      const volatile float *pv = a.am_val;
-      const volatile int32_t *pi = a.am_idx;
-      for (int b = tid; b < (int)gridDim.x; b += 256) {
-        const float v = pv[b];
-        const int i = pi[b];
-        if (am_better(v, i, bv, bi)) bv = v, bi = i;
-      }
-      am_wave(bv, bi);
-      if (lane == 0) red_v[wid] = bv, red_i[wid] = bi;
-      __syncthreads();
-      if (tid == 0) {
-        bv = red_v[0];
-        bi = red_i[0];
-        for (int w = 1; w < 4; ++w)
-          if (am_better(red_v[w], red_i[w], bv, bi)) bv = red_v[w], bi = red_i[w];
-        *a.am_out = bi;
-        *a.am_counter = 0u;
-      }
-    }
-  }
+  if constexpr (EPI == EPI_ARGMAX) am_partial(best_v, best_i, a.am_val, a.am_idx);
 }
 
 // ------------------------------------------------------- generic rows ----
@@ -226,55 +259,14 @@ __global__ void k_dequant(const uint8_t *W, int64_t offset, int64_t n, float *ou
 // ----------------------------------------------------------------- argmax ----
 // FloatTensor.kt:53-66 over v[0..n): per-block partials, the last block to
 // arrive reduces them in block order and resets the counter.
-__global__ __launch_bounds__(256) void k_argmax(const float *v, int32_t n, float *part_val, int32_t *part_idx,
-                                                uint32_t *counter, int32_t *out) {
-  __shared__ float rv[4];
-  __shared__ int ri[4];
-  __shared__ bool is_last;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+__global__ __launch_bounds__(256) void k_argmax(const float *v, int32_t n, float *part_val, int32_t *part_idx) {
   float bv = -__builtin_inff();
   int bi = INT_MAX;
-  for (int i = blockIdx.x * 256 + tid; i < n; i += gridDim.x * 256) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
     const float k = am_key(v[i], i);
     if (am_better(k, i, bv, bi)) bv = k, bi = i;
   }
-  am_wave(bv, bi);
-  if (lane == 0) rv[wid] = bv, ri[wid] = bi;
-  __syncthreads();
-  if (tid == 0) {
-    bv = rv[0];
-    bi = ri[0];
-    for (int w = 1; w < 4; ++w)
-      if (am_better(rv[w], ri[w], bv, bi)) bv = rv[w], bi = ri[w];
-    part_val[blockIdx.x] = bv;
-    part_idx[blockIdx.x] = bi;
-    __threadfence();
-    is_last = atomicAdd(counter, 1u) == gridDim.x - 1;
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  bv = -__builtin_inff();
-  bi = INT_MAX;
-  const volatile float *pv = part_val;
-  const volatile int32_t *pi = part_idx;
-  for (int b = tid; b < (int)gridDim.x; b += 256) {
-    const float vv = pv[b];
-    const int ii = pi[b];
-    if (am_better(vv, ii, bv, bi)) bv = vv, bi = ii;
-  }
-  am_wave(bv, bi);
-  __syncthreads();
-  if (lane == 0) rv[wid] = bv, ri[wid] = bi;
-  __syncthreads();
-  if (tid == 0) {
-    bv = rv[0];
-    bi = ri[0];
-    for (int w = 1; w < 4; ++w)
-      if (am_better(rv[w], ri[w], bv, bi)) bv = rv[w], bi = ri[w];
-    *out = bi;
-    *counter = 0u;
-  }
+  am_partial(bv, bi, part_val, part_idx);
 }
 
 // ------------------------------------------------------------------ route ----
@@ -362,31 +354,62 @@ bool rows_fast_ok(int type, const RowsArgs &a, bool paired) {
   if ((a.base0 % 64) != 0 || (a.row_stride % 64) != 0 || (a.expert_stride % 64) != 0) return false;
   if (paired && (a.base1 % 64) != 0) return false;
   if (paired && (a.dim1 / 64) > 64) return false;  // paired epilogue needs a single column pass
+  if (paired && type == T_F32) return false;         // one row step per F32 tile: no room for the pair
   switch (type) {
     case T_Q8_0: case T_Q4_0: case T_Q4_K: case T_F16: case T_BF16: case T_F32: return true;
     default: return false;
   }
 }
 
-int max_argmax_blocks(const DevInfo &dev) { return dev.cu_count * 2; }
+int max_argmax_blocks(const DevInfo &dev) { return dev.cu_count * 8; }
 
-template <class F, int LPR>
-static hipError_t launch_fast_lpr(int epi, const RowsArgs &a, int segments, const DevInfo &dev, hipStream_t s) {
-  constexpr int RT = F::RT, RPW = 64 / LPR, TR = RT * RPW;
+template <class F, int LPR, int CPL>
+static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, const DevInfo &dev, hipStream_t s) {
+  constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1, RPW = 64 / LPR, TR = RT * RPW;
+  typedef void (*Kernel)(RowsArgs);
+  const bool multi = (a.dim1 / 64) > LPR * CPL;
+  Kernel k = nullptr;
+  if (epi == EPI_STORE) {
+    k = k_rows<F, LPR, CPL, EPI_STORE, false>;
+    if constexpr (LPR == 64 && CPL == 2)
+      if (multi) k = k_rows<F, LPR, CPL, EPI_STORE, true>;
+  } else if (epi == EPI_ARGMAX) {
+    k = k_rows<F, LPR, CPL, EPI_ARGMAX, false>;
+    if constexpr (LPR == 64 && CPL == 2)
+      if (multi) k = k_rows<F, LPR, CPL, EPI_ARGMAX, true>;
+  } else {
+    if constexpr (CPL == 1 && F::RT >= 2) k = k_rows<F, LPR, 1, EPI_GELU_PAIR, false>;
+  }
+  if (!k) return hipErrorInvalidValue;
+  if (multi && !(LPR == 64 && CPL == 2)) return hipErrorInvalidValue;
+
+  // Resident 256-thread workgroups per CU for this kernel (register-limited);
+  // the launch fills exactly that many waves when there are tiles enough.
+  static int resident[3][2];
+  int &res = resident[epi][multi ? 1 : 0];
+  if (res == 0) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 256, 0) != hipSuccess || nb < 1) nb = 2;
+    res = nb;
+  }
   const int lrt = epi == EPI_GELU_PAIR ? TR / 2 : TR;
-  const int n_tiles = (a.rows + lrt - 1) / lrt;
-  // target ~8 waves (two per SIMD) per CU over the whole launch
-  int max_blocks = dev.cu_count * 2 / (segments > 0 ? segments : 1);
-  if (max_blocks < 1) max_blocks = 1;
-  if (epi == EPI_ARGMAX) max_blocks = max_argmax_blocks(dev);
-  int blocks = (n_tiles + 3) / 4;
-  if (blocks > max_blocks) blocks = max_blocks;
-  if (blocks < 1) blocks = 1;
-  dim3 grid(blocks, segments);
-  switch (epi) {
-    case EPI_STORE: hipLaunchKernelGGL((k_rows<F, LPR, EPI_STORE>), grid, dim3(256), 0, s, a); break;
-    case EPI_ARGMAX: hipLaunchKernelGGL((k_rows<F, LPR, EPI_ARGMAX>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((k_rows<F, LPR, EPI_GELU_PAIR>), grid, dim3(256), 0, s, a); break;
+  const int64_t n_tiles = (a.rows + lrt - 1) / lrt;
+  const int64_t segs = segments > 0 ? segments : 1;
+  const int64_t cu = dev.cu_count;
+  int64_t waves = cu * res * 4 / segs;
+  if (waves < 1) waves = 1;
+  if (waves > n_tiles) waves = n_tiles > 0 ? n_tiles : 1;
+  // spread the waves over every CU: 1, 2 or 4 waves per workgroup
+  const int64_t total = waves * segs;
+  const int wpb = total >= 4 * cu ? 4 : (total >= 2 * cu ? 2 : 1);
+  int64_t blocks = (waves + wpb - 1) / wpb;
+  if (epi == EPI_ARGMAX && blocks > max_argmax_blocks(dev)) blocks = max_argmax_blocks(dev);
+  hipLaunchKernelGGL(k, dim3((unsigned)blocks, (unsigned)segments), dim3(64 * wpb), 0, s, a);
+  if (epi == EPI_ARGMAX) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, (const float *)a.am_val, (const int32_t *)a.am_idx,
+                       (int)blocks, a.am_out);
   }
   return hipGetLastError();
 }
@@ -394,9 +417,11 @@ static hipError_t launch_fast_lpr(int epi, const RowsArgs &a, int segments, cons
 template <class F>
 static hipError_t launch_fast(int epi, const RowsArgs &a, int segments, const DevInfo &dev, hipStream_t s) {
   const int C = a.dim1 / 64;
-  if (C > 32) return launch_fast_lpr<F, 64>(epi, a, segments, dev, s);
-  if (C > 16) return launch_fast_lpr<F, 32>(epi, a, segments, dev, s);
-  return launch_fast_lpr<F, 16>(epi, a, segments, dev, s);
+  // single column pass up to 64 lanes x 2 chunks = 8192 columns; passes beyond that
+  if (C > 64 && epi != EPI_GELU_PAIR) return launch_fast_cfg<F, 64, 2>(epi, a, segments, dev, s);
+  if (C > 32) return launch_fast_cfg<F, 64, 1>(epi, a, segments, dev, s);
+  if (C > 16) return launch_fast_cfg<F, 32, 1>(epi, a, segments, dev, s);
+  return launch_fast_cfg<F, 16, 1>(epi, a, segments, dev, s);
 }
 
 template <int TYPE>
@@ -452,7 +477,7 @@ hipError_t launch_rows(int type, int epi, const RowsArgs &a, int segments, const
   }
   hipError_t e = launch_generic(type, a, 1, segments, dev, s);
   if (e != hipSuccess || epi != EPI_ARGMAX) return e;
-  return launch_argmax(a.y, a.rows, a.am_val, a.am_idx, a.am_counter, a.am_out, dev, s);
+  return launch_argmax(a.y, a.rows, a.am_val, a.am_idx, a.am_out, dev, s);
 }
 
 hipError_t launch_dequant(int type, const uint8_t *W, int64_t offset, int64_t n, float *out, hipStream_t s) {
@@ -470,13 +495,17 @@ hipError_t launch_dequant(int type, const uint8_t *W, int64_t offset, int64_t n,
   return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float *v, int32_t n, float *part_val, int32_t *part_idx, uint32_t *counter,
-                         int32_t *out, const DevInfo &dev, hipStream_t s) {
+hipError_t launch_argmax(const float *v, int32_t n, float *part_val, int32_t *part_idx, int32_t *out,
+                         const DevInfo &dev, hipStream_t s) {
   int blocks = (n + 255) / 256;
   const int cap = max_argmax_blocks(dev);
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(k_argmax, dim3(blocks), dim3(256), 0, s, v, n, part_val, part_idx, counter, out);
+  hipLaunchKernelGGL(k_argmax, dim3(blocks), dim3(256), 0, s, v, n, part_val, part_idx);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, (const float *)part_val, (const int32_t *)part_idx,
+                     blocks, out);
   return hipGetLastError();
 }
 

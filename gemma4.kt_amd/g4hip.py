@@ -101,6 +101,8 @@ SIGNATURES = {
     "g4_dequant_dev": [_vp, _vp, _i64, _i64, _vp],
     "g4_ffn": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32],
     "g4_ffn_dev": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32],
+    "g4_ffn_gate_up": [_vp, _vp, _vp, _vp, _vp, _i32, _i32],
+    "g4_ffn_gate_up_dev": [_vp, _vp, _vp, _vp, _vp, _i32, _i32],
     "g4_moe_route": [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp],
     "g4_moe_route_dev": [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp],
     "g4_moe": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp],
@@ -388,6 +390,20 @@ def ffn(ctx: Context, gate: GpuFloatTensor, up: GpuFloatTensor, down: GpuFloatTe
 def ffn_dev(ctx: Context, gate, up, down, x, y, dim: int, hidden: int) -> None:
     check(lib().g4_ffn_dev(ctx.handle, gate.handle, up.handle, down.handle, _ptr(_dev_f32(x, "x")),
                            _ptr(_dev_f32(y, "y")), int(dim), int(hidden)))
+
+
+def ffn_gate_up(ctx: Context, gate: GpuFloatTensor, up: GpuFloatTensor, x: np.ndarray, dim: int,
+                hidden: int) -> np.ndarray:
+    """h = gelu(gate x) * (up x) (Llama.kt:357-360)."""
+    _f32(x, "x")
+    h = np.empty(hidden, dtype=np.float32)
+    check(lib().g4_ffn_gate_up(ctx.handle, gate.handle, up.handle, _ptr(x), _ptr(h), int(dim), int(hidden)))
+    return h
+
+
+def ffn_gate_up_dev(ctx: Context, gate, up, x, h, dim: int, hidden: int) -> None:
+    check(lib().g4_ffn_gate_up_dev(ctx.handle, gate.handle, up.handle, _ptr(_dev_f32(x, "x")),
+                                   _ptr(_dev_f32(h, "h")), int(dim), int(hidden)))
 
 
 def moe_route(ctx: Context, logits: np.ndarray, k: int, renormalize: bool,

@@ -129,6 +129,12 @@ int g4_ffn(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const g4
            float *y, int32_t dim, int32_t hidden);
 int g4_ffn_dev(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const g4_weight *w_down,
                const float *d_x, float *d_y, int32_t dim, int32_t hidden);
+/* The first half of that FFN (Llama.kt:357-360): h = gelu(w_gate x) * (w_up x),
+ * h: float[hidden].  One fused launch; g4_ffn is this plus g4_matmul of w_down. */
+int g4_ffn_gate_up(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const float *x, float *h,
+                   int32_t dim, int32_t hidden);
+int g4_ffn_gate_up_dev(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const float *d_x, float *d_h,
+                       int32_t dim, int32_t hidden);
 
 /* MoE routing of T tokens (Llama.kt:269-293): per token softmax over n_experts
  * router logits (MutableFloatTensor.kt:54-59, exp in double), top-k by repeated
