@@ -64,12 +64,16 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   constexpr int TR = RT * RPW;                   // physical rows per tile
   constexpr int LRT = (EPI == EPI_GELU_PAIR) ? TR / 2 : TR;  // logical rows per tile
   constexpr int NDW = F::NDW;
+  constexpr int NCH = LPR * CPL;                 // x chunks of one column pass
+  constexpr int XSEG = NCH * 16 / 256;           // 16-byte x segments each of the 256 threads stages
   static_assert(RT >= 1, "tile");
   static_assert(EPI != EPI_GELU_PAIR || (RT >= 2 && CPL == 1), "paired tiles: gate and up steps, one pass");
+  static_assert(XSEG >= 1 && XSEG * 256 == NCH * 16, "x staging");
+  __shared__ u32x4 xl[NCH * 16];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: tile loop control stays scalar
-  const int wpb = blockDim.x >> 6;
+  constexpr int wpb = 4;                         // launched with 256 threads
   const int gi = lane / LPR, q = lane % LPR;
   const int seg = blockIdx.y;
   const int expert = a.ids ? a.ids[seg] : 0;
@@ -79,7 +83,9 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   float *y = a.y ? a.y + (int64_t)seg * a.y_stride : nullptr;
 
   const int n_tiles = (a.rows + LRT - 1) / LRT;
-  const int nwv = gridDim.x * wpb, wv = blockIdx.x * wpb + wid;
+  // wave wid of block b is virtual wave wid * blocks + b: when there are fewer
+  // tiles than waves, every workgroup (so every CU) still gets some
+  const int nwv = gridDim.x * wpb, wv = wid * gridDim.x + blockIdx.x;
   const int tpw = (n_tiles + nwv - 1) / nwv;
   const int t0 = min(n_tiles, wv * tpw), t1 = min(n_tiles, t0 + tpw);
   const int C = a.dim1 >> 6;
@@ -170,27 +176,43 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     uint32_t DA[RT][CPL][NDW], DB[RT][CPL][NDW];
     bool okA[RT][CPL], okB[RT][CPL];
     int64_t EA[RT][CPL], EB[RT][CPL];
-    // This lane's x columns first, straight from global memory (x is small and
-    // L2-resident after the first wave touches it); the weight loads go out
-    // right after, so the wait for x (vmcnt retires in issue order) never
-    // covers the weight latency, and no workgroup barrier is needed.
+    // x of this pass, once per workgroup: each thread fetches XSEG 16-byte
+    // segments (coalesced), then the first weight tile goes out, and only then
+    // does the thread wait for x (vmcnt retires in issue order, so that wait
+    // never covers the weight latency; the barrier waits on LDS only).
+    u32x4a4 xr[XSEG];
+#pragma unroll
+    for (int j = 0; j < XSEG; ++j) {
+      const int s = j * 256 + tid, c = pass * NCH + (s >> 4);
+      // dword alignment is all a caller's x guarantees; gfx950 takes 128-bit loads at that alignment
+      xr[j] = ((const u32x4a4 *)(x + (int64_t)(c < C ? c : 0) * 64))[s & 15];
+    }
+    load_tile(t0, pass, t0 < t1, DA, okA, EA);
+    if (MULTI && pass > 0) __syncthreads();  // every wave has read the previous pass's x
+#pragma unroll
+    for (int j = 0; j < XSEG; ++j) {
+      const int s = j * 256 + tid, ch = s >> 4, c = pass * NCH + ch;
+      // zeroed by a mask, not a select: a select lets the compiler sink the
+      // load into a branch, whose wait would then cover the weight loads too
+      const uint32_t m = opaque(c < C ? ~0u : 0u);
+      xl[ch * 16 + ((s & 15) ^ (ch & 15))] = u32x4{xr[j].x & m, xr[j].y & m, xr[j].z & m, xr[j].w & m};
+    }
+    __syncthreads();
+    // chunk ch's 16-byte segment i sits at slot i ^ (ch & 15): the 8 lanes one
+    // LDS cycle serves read 8 different bank groups
     float xv[CPL][64];
 #pragma unroll
     for (int u = 0; u < CPL; ++u) {
-      const int c = (pass * CPL + u) * LPR + q;
-      const bool in = c < C;
-      // dword alignment is all a caller's x guarantees; gfx950 takes 128-bit loads at that alignment
-      const u32x4a4 *xp = (const u32x4a4 *)(x + (int64_t)(in ? c : 0) * 64);
+      const int ch = u * LPR + q;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const u32x4a4 t = xp[i];
-        xv[u][4 * i] = in ? __uint_as_float(t.x) : 0.f;
-        xv[u][4 * i + 1] = in ? __uint_as_float(t.y) : 0.f;
-        xv[u][4 * i + 2] = in ? __uint_as_float(t.z) : 0.f;
-        xv[u][4 * i + 3] = in ? __uint_as_float(t.w) : 0.f;
+        const u32x4 t = xl[ch * 16 + (i ^ (ch & 15))];
+        xv[u][4 * i] = __uint_as_float(t.x);
+        xv[u][4 * i + 1] = __uint_as_float(t.y);
+        xv[u][4 * i + 2] = __uint_as_float(t.z);
+        xv[u][4 * i + 3] = __uint_as_float(t.w);
       }
     }
-    load_tile(t0, pass, t0 < t1, DA, okA, EA);
     float xs[CPL][F::NS > 0 ? F::NS : 1];
 #pragma unroll
     for (int u = 0; u < CPL; ++u) F::sums(xv[u], xs[u]);
@@ -396,15 +418,15 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
   const int64_t n_tiles = (a.rows + lrt - 1) / lrt;
   const int64_t segs = segments > 0 ? segments : 1;
   const int64_t cu = dev.cu_count;
-  int64_t waves = cu * res * 4 / segs;
-  if (waves < 1) waves = 1;
-  if (waves > n_tiles) waves = n_tiles > 0 ? n_tiles : 1;
-  // spread the waves over every CU: 1, 2 or 4 waves per workgroup
-  const int64_t total = waves * segs;
-  const int wpb = total >= 4 * cu ? 4 : (total >= 2 * cu ? 2 : 1);
-  int64_t blocks = (waves + wpb - 1) / wpb;
+  // 4-wave workgroups sharing one LDS copy of x; at least one workgroup per CU
+  // (idle waves only help stage x), never more workgroups than tiles
+  int64_t blocks = (cu * res * 4 / segs + 3) / 4;
+  const int64_t spread = (cu + segs - 1) / segs;
+  if (blocks < spread) blocks = spread;
+  if (blocks > n_tiles) blocks = n_tiles;
+  if (blocks < 1) blocks = 1;
   if (epi == EPI_ARGMAX && blocks > max_argmax_blocks(dev)) blocks = max_argmax_blocks(dev);
-  hipLaunchKernelGGL(k, dim3((unsigned)blocks, (unsigned)segments), dim3(64 * wpb), 0, s, a);
+  hipLaunchKernelGGL(k, dim3((unsigned)blocks, (unsigned)segments), dim3(256), 0, s, a);
   if (epi == EPI_ARGMAX) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
