@@ -155,7 +155,7 @@ struct FmtQ8_0 {
 // (16 q, exact) and the 1/16 folded into the block sum; -8 enters through the
 // precomputed sum of x.
 struct FmtQ4_0 {
-  static constexpr int TYPE = T_Q4_0, NDW = 9, NS = 2, RT = 4;
+  static constexpr int TYPE = T_Q4_0, NDW = 9, NS = 2, RT = 2;
   G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
     const uint8_t *p = W + (e >> 6) * 36;
     const u32x4a4 *v = (const u32x4a4 *)p;
@@ -202,7 +202,7 @@ struct FmtQ4_0 {
 // nibbles sub-block 2g+1; w = d*sc*q - dmin*m (Q4_KFloatTensor.kt:23-55).
 // Per sub-block: d*sc * sum(x q) - dmin*m * sum(x).
 struct FmtQ4_K {
-  static constexpr int TYPE = T_Q4_K, NDW = 12, NS = 2, RT = 4;
+  static constexpr int TYPE = T_Q4_K, NDW = 12, NS = 2, RT = 2;
   G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
     int64_t G = e >> 6;
     const uint8_t *sb = W + (G >> 2) * 144;

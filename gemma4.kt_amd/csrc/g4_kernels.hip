@@ -418,11 +418,15 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
   const int64_t n_tiles = (a.rows + lrt - 1) / lrt;
   const int64_t segs = segments > 0 ? segments : 1;
   const int64_t cu = dev.cu_count;
-  // 4-wave workgroups sharing one LDS copy of x; at least one workgroup per CU
-  // (idle waves only help stage x), never more workgroups than tiles
-  int64_t blocks = (cu * res * 4 / segs + 3) / 4;
-  const int64_t spread = (cu + segs - 1) / segs;
-  if (blocks < spread) blocks = spread;
+  // 4-wave workgroups sharing one LDS copy of x.  About two tiles per wave (one
+  // computing while the next is in flight), rounded up to whole rounds of one
+  // workgroup per CU over all segments (a partial round leaves CUs with half
+  // the work of the others), at most what is resident at once, never more
+  // workgroups than tiles (idle waves only help stage x).
+  int64_t blocks = (n_tiles + 7) / 8;
+  blocks = ((blocks * segs + cu - 1) / cu * cu + segs - 1) / segs;
+  const int64_t cap = cu * res / segs;
+  if (blocks > cap) blocks = cap;
   if (blocks > n_tiles) blocks = n_tiles;
   if (blocks < 1) blocks = 1;
   if (epi == EPI_ARGMAX && blocks > max_argmax_blocks(dev)) blocks = max_argmax_blocks(dev);
