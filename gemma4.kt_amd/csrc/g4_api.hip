@@ -204,6 +204,22 @@ int batch_dev(g4_ctx *ctx, const g4_weight *w, int64_t off, const float *d_X, in
     G4_HIP(hipMemsetAsync(d_Y, 0, sizeof(float) * (size_t)dim0 * M, ctx->stream), "hipMemsetAsync");
     return G4_OK;
   }
+  // several tokens: the matrix-core kernel unpacks each weight once for all of them
+  if (M >= 2) {
+    g4::TokArgs t;
+    t.W = w->d;
+    t.base = off;
+    t.row_stride = dim1;
+    t.rows = dim0;
+    t.dim1 = dim1;
+    t.x = d_X;
+    t.x_stride = dim1;
+    t.M = M;
+    t.y = d_Y;
+    t.y_stride = dim0;
+    if (g4::tok_ok(w->type, t))
+      return launch_status(g4::launch_tok(w->type, t, ctx->dev, ctx->stream), "matmul_batch");
+  }
   g4::RowsArgs a = plain_rows(w, off, d_X, d_Y, dim0, dim1);
   a.x_stride = dim1;
   a.y_stride = dim0;

@@ -428,9 +428,6 @@ G4_DEV void am_wave(float &v, int &i) {
   am_step<1>(v, i, lane);
 }
 
-// Coherent (L2) load that does not serialise like a volatile access.
-G4_DEV float load_agent(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-G4_DEV int load_agent(const int32_t *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 // Llama.kt:23-25 gelu, evaluated in double like the reference.
 G4_DEV float gelu_ref(float xf) {

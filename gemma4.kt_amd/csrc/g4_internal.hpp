@@ -52,6 +52,25 @@ hipError_t launch_rows(int type, int epi, const RowsArgs &a, int segments, const
                        hipStream_t stream);
 int max_argmax_blocks(const DevInfo &dev);
 
+// Multi-token matmul on the matrix cores: y[m * y_stride + r] = W row r . x_m for
+// m < M, row r starting at element base + r * row_stride, x_m = x + m * x_stride.
+struct TokArgs {
+  const uint8_t *W;
+  int64_t base;
+  int64_t row_stride;
+  int32_t rows;
+  int32_t dim1;
+  const float *x;
+  int64_t x_stride;
+  int32_t M;
+  float *y;
+  int64_t y_stride;
+};
+
+// True when (type, offsets, dim1) take the matrix-core kernel (Q4_K, 64-element aligned rows).
+bool tok_ok(int type, const TokArgs &a);
+hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_t stream);
+
 hipError_t launch_dequant(int type, const uint8_t *W, int64_t offset, int64_t n, float *out, hipStream_t stream);
 hipError_t launch_argmax(const float *v, int32_t n, float *part_val, int32_t *part_idx, int32_t *out,
                          const DevInfo &dev, hipStream_t stream);

@@ -130,6 +130,22 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   float best_v = -__builtin_inff();
   int best_i = INT_MAX;
 
+  // EPI_GELU_PAIR: the (gate, up) pair of each finished row waits in a per-wave
+  // LDS queue, and gelu (in double, like the reference) runs once per 64 rows
+  // with every lane busy rather than once per tile with one lane per row.  The
+  // queued rows are contiguous because a wave finishes its tiles in order.
+  __shared__ float2 gq[EPI == EPI_GELU_PAIR ? 4 : 1][64];
+  int gq_n = 0, gq_row = t0 * LRT;
+  auto gq_flush = [&]() {
+    if (lane < gq_n) {
+      const float2 p = gq[EPI == EPI_GELU_PAIR ? wid : 0][lane];
+      const int lr = gq_row + lane;
+      if (lr < a.rows) y[lr] = gelu_ref(p.x) * p.y;
+    }
+    gq_row += gq_n;
+    gq_n = 0;
+  };
+
   auto finish_tile = [&](int t, int pass, const uint32_t (&D)[RT][CPL][NDW], const bool (&ok)[RT][CPL],
                          const int64_t (&E)[RT][CPL], const float (&xv)[CPL][64], const float (&xs)[CPL][F::NS > 0 ? F::NS : 1]) {
     float v[RT];
@@ -148,8 +164,9 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     const bool writer = (q % (LPR / RT)) == 0;
     if constexpr (EPI == EPI_GELU_PAIR) {
       const float up = __shfl_xor(r, LPR / 2, 64);
-      const int lr = t * LRT + (k % (RT / 2)) * RPW + gi;
-      if (writer && k < RT / 2 && lr < a.rows) y[lr] = gelu_ref(r) * up;
+      if (writer && k < RT / 2) gq[wid][gq_n + (k % (RT / 2)) * RPW + gi] = make_float2(r, up);
+      gq_n += LRT;
+      if (gq_n + LRT > 64) gq_flush();
     } else {
       const int lr = t * LRT + k * RPW + gi;
       if (writer && lr < a.rows) {
@@ -218,7 +235,9 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     for (int u = 0; u < CPL; ++u) F::sums(xv[u], xs[u]);
 
     // software pipeline: tile t+1 is in flight while tile t is unpacked and
-    // reduced.  The scheduling barriers keep the compiler from sinking the next
+    // reduced (only the first tile goes out with x: issuing the second one too
+    // delays every wave's first tile behind the others' second, measured
+    // slower).  The scheduling barriers keep the compiler from sinking the next
     // tile's loads into the current tile's arithmetic.
     for (int t = t0; t < t1; t += 2) {
       load_tile(t + 1, pass, t + 1 < t1, DB, okB, EB);
@@ -232,6 +251,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     }
   }
 
+  if constexpr (EPI == EPI_GELU_PAIR) gq_flush();
   if constexpr (EPI == EPI_ARGMAX) am_partial(best_v, best_i, a.am_val, a.am_idx);
 }
 
@@ -309,7 +329,8 @@ G4_DEV float java_max(float a, float b) {
 __global__ __launch_bounds__(64) void k_route(const float *logits, int32_t E, int32_t K, int32_t renorm,
                                               const float *expert_scale, int32_t *ids, float *weights) {
   __shared__ float p[ROUTE_MAX_E];
-  __shared__ float sum_s;
+  __shared__ float pick_w[ROUTE_MAX_E];
+  __shared__ int32_t pick_i[ROUTE_MAX_E];
   const int t = blockIdx.x, lane = threadIdx.x;
   const float *lg = logits + (int64_t)t * E;
   float m = -__builtin_inff();
@@ -318,15 +339,14 @@ __global__ __launch_bounds__(64) void k_route(const float *logits, int32_t E, in
   for (int s = 32; s >= 1; s >>= 1) m = java_max(m, __shfl_xor(m, s, 64));
   for (int i = lane; i < E; i += 64) p[i] = (float)exp((double)__fsub_rn(lg[i], m));
   __syncthreads();
-  if (lane == 0) {
-    float s = 0.f;
-    for (int i = 0; i < E; ++i) s = __fadd_rn(s, p[i]);
-    sum_s = s;
-  }
+  // fp32 sum in index order: every lane adds the same sequence (LDS broadcast
+  // reads), so the sum needs no second barrier
+  float sum = 0.f;
+  for (int i = 0; i < E; ++i) sum = __fadd_rn(sum, p[i]);
   __syncthreads();
-  const float sum = sum_s;
   for (int i = lane; i < E; i += 64) p[i] = __fdiv_rn(p[i], sum);
   __syncthreads();
+  // the picks stay in LDS; every lane keeps the same running renormalisation sum
   float renorm_sum = 0.f;
   for (int j = 0; j < K; ++j) {
     float bv = -__builtin_inff();
@@ -337,22 +357,22 @@ __global__ __launch_bounds__(64) void k_route(const float *logits, int32_t E, in
     }
     am_wave(bv, bi);
     if (bv == -__builtin_inff()) bi = 0;  // no entry beats the initial -inf: the scan keeps index 0
+    renorm_sum = __fadd_rn(renorm_sum, bv);
     __syncthreads();
     if (lane == 0) {
-      ids[(int64_t)t * K + j] = bi;
-      weights[(int64_t)t * K + j] = bv;
+      pick_i[j] = bi;
+      pick_w[j] = bv;
       p[bi] = -__builtin_inff();
-      renorm_sum = __fadd_rn(renorm_sum, bv);
     }
     __syncthreads();
   }
-  if (lane == 0) {
-    for (int j = 0; j < K; ++j) {
-      float w = weights[(int64_t)t * K + j];
-      if (renorm) w = __fdiv_rn(w, renorm_sum);
-      if (expert_scale) w = __fmul_rn(w, expert_scale[ids[(int64_t)t * K + j]]);
-      weights[(int64_t)t * K + j] = w;
-    }
+  for (int j = lane; j < K; j += 64) {
+    const int id = pick_i[j];
+    float w = pick_w[j];
+    if (renorm) w = __fdiv_rn(w, renorm_sum);
+    if (expert_scale) w = __fmul_rn(w, expert_scale[id]);
+    ids[(int64_t)t * K + j] = id;
+    weights[(int64_t)t * K + j] = w;
   }
 }
 

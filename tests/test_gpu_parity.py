@@ -253,6 +253,38 @@ def test_q4_k_batched(g4, ctx, oracle, m):
         assert_dots(Y[i][rows], ex[rows], ab[rows], "batched m=%d row %d" % (m, i))
 
 
+# matrix-core multi-token kernel: partial row and token tiles, several column
+# passes (dim1 > 2048), rows that start mid super-block (1408 = 5.5 super-blocks),
+# a row offset, a single 64-column group
+@pytest.mark.parametrize("m,rows,dim1,off_rows", [
+    (2, 40, 2048, 0), (17, 34, 4224, 0), (5, 34, 1408, 0), (16, 48, 2048, 3), (3, 20, 64, 0)])
+def test_q4_k_batched_matrix_core_shapes(g4, ctx, oracle, m, rows, dim1, off_rows):
+    announce("q4_k batched M=%d rows=%d dim1=%d off_rows=%d" % (m, rows, dim1, off_rows))
+    n = (rows + off_rows) * dim1
+    raw = synth.weights(52, "mc%d.%d" % (rows, dim1), Q4_K, n)
+    X = synth.activations(52, "mcx%d.%d" % (m, dim1), m * dim1).reshape(m, dim1)
+    w = upload(g4, ctx, Q4_K, raw, n)
+    off = off_rows * dim1
+    Y = w.matmul_batch(X, rows, dim1, off)
+    for i in range(m):
+        ex, ab = oracle.matmul_exact(Q4_K, raw, X[i], rows, dim1, off)
+        assert_dots(Y[i], ex, ab, "token %d" % i)
+
+
+def test_q4_k_batched_matrix_core_wide_range_x(g4, ctx, oracle):
+    """x spanning 1e-20..1e20: the three bf16 parts of x are exact at every magnitude."""
+    announce("q4_k batched wide-range x")
+    m, rows, dim1 = 4, 32, 2048
+    raw = synth.weights(53, "mcw", Q4_K, rows * dim1)
+    rng = np.random.default_rng(53)
+    X = (rng.standard_normal((m, dim1)) * 10.0 ** rng.uniform(-20, 20, (m, dim1))).astype(np.float32)
+    w = upload(g4, ctx, Q4_K, raw, rows * dim1)
+    Y = w.matmul_batch(X, rows, dim1)
+    for i in range(m):
+        ex, ab = oracle.matmul_exact(Q4_K, raw, X[i], rows, dim1)
+        assert_dots(Y[i], ex, ab, "token %d" % i)
+
+
 @pytest.mark.parametrize("tokens", [1, 16])
 @pytest.mark.parametrize("renorm", [True, False])
 def test_moe_route_exact(g4, ctx, oracle, tokens, renorm):
