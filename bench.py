@@ -38,6 +38,22 @@ MALL_BYTES = 256 << 20
 Q8_0, Q4_0, Q4_K = 8, 2, 12
 
 
+# HBM bytes per launch of each workload's timed kernel (or launch group), from two
+# rocprofv3 --pmc passes over `bench.py --eager`: FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0
+# (KiB), the factors being what the counters read for a plain 256 MiB fp32 copy.
+# Recorded in profiles/hbm_traffic_fetch_write_size.md (same command and kernels).
+TRAFFIC_BYTES = {
+    "q4_0_ffn_decode_token": 19169075,
+    "q8_0_matvec_2048x2048": 4645683,
+    "q8_0_lm_head_262144x2048_argmax": 577968640,
+    "q4_k_batched_8192x2048_m1": 9658163,
+    "q4_k_batched_8192x2048_m8": 10421043,
+    "q4_k_batched_8192x2048_m64": 15926067,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40050483,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 593801728,
+}
+
+
 def copies_for(nbytes: int, cap: int = 256) -> int:
     """Weight copies so that one pass over them spans >= 2x the Infinity Cache."""
     if nbytes >= 2 * MALL_BYTES:
@@ -226,7 +242,7 @@ class BatchedQ4_K(Workload):
 
 class MoeQ4_K(Workload):
     unit = "tokens/s"
-    dominant_name = "k_rows<FmtQ4_K, 32, EPI_GELU_PAIR> (expert gate+up)"
+    dominant_name = "expert launches of g4_moe: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR> + k_rows<FmtQ4_K, 32> + k_moe_combine"
 
     def __init__(self, g4, ctx, torch, tokens=1, routings=32):
         import synth
@@ -254,7 +270,9 @@ class MoeQ4_K(Workload):
         self.per_expert = per_expert
         mean_distinct = float(np.mean(self.distinct))
         self.step_bytes = int(mean_distinct * per_expert + 4 * tokens * (D + E + D))
-        self.dominant_bytes = int(mean_distinct * (2 * FF * D // 256 * 144))
+        # the timed group (g4_moe) reads every routed expert's gate_up and down once,
+        # x, and writes Y; the router logits belong to the separate route launch
+        self.dominant_bytes = int(mean_distinct * per_expert + 4 * tokens * (D + D))
         self.tokens_per_step = tokens
         self.g4, self.ctx = g4, ctx
 
@@ -284,8 +302,33 @@ class MoeQ4_K(Workload):
                 "algorithmic_bytes_per_step": self.step_bytes}
 
 
+class CopyCalibration(Workload):
+    """A plain fp32 copy of known size (y = x * 1 through torch's elementwise kernel).
+
+    Not part of --all: it is the reference point that scales the FETCH_SIZE /
+    WRITE_SIZE counters into HBM bytes (each counter divided by what it reads
+    for exactly 256 MiB in and 256 MiB out)."""
+    name = "copy_256MiB_f32"
+    dominant_name = "vectorized_elementwise_kernel (y = x * 1)"
+
+    def __init__(self, g4, ctx, torch):
+        n = 64 << 20
+        self.x = torch.ones(n, dtype=torch.float32, device="cuda")
+        self.y = torch.empty_like(self.x)
+        self.step_bytes = self.dominant_bytes = 2 * 4 * n
+        self.torch = torch
+
+    def step(self, i):
+        self.torch.mul(self.x, 1.0, out=self.y)
+
+    def config(self):
+        return {"workload": self.name, "bytes_read": self.step_bytes // 2, "bytes_written": self.step_bytes // 2}
+
+
 def make_workload(spec: str, g4, ctx, torch) -> Workload:
     name, _, arg = spec.partition(":")
+    if name == "copy":
+        return CopyCalibration(g4, ctx, torch)
     if name == "q4_0_ffn":
         return FfnQ4_0(g4, ctx, torch)
     if name == "q8_0_matvec":
@@ -422,11 +465,11 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool)
         "config": dict(wl.config(), graph=step_graph is not None, step_gbs=round(gbs_step, 2),
                        hbm_fraction=round(gbs_step / HBM_PEAK_GBS, 4)),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES.get(wl.name),
                      "kernel": wl.dominant_name, "bytes_per_launch": wl.dominant_bytes,
                      "avg_launch_us": round(kern_ms * 1e3, 3), "launches_timed": launches},
     }
-    if cpu_seconds > 0:
+    if cpu_seconds > 0 and not isinstance(wl, CopyCalibration):
         line["cpu_baseline"] = cpu_baseline(wl, cpu_seconds)
     ctx.close()
     return line
@@ -437,7 +480,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--workload", default="q4_0_ffn")
+    ap.add_argument("--workload", default="q4_0_ffn", help="workload spec, or several separated by commas")
     ap.add_argument("--all", action="store_true", help="one JSON line per workload")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (0 = skip)")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
@@ -446,7 +489,7 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (each box has one MI355X); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
-    specs = [args.workload]
+    specs = args.workload.split(",")
     if args.all:
         specs = ["q4_0_ffn", "q8_0_matvec", "q8_0_lm_head", "q4_k_batched:1", "q4_k_batched:8",
                  "q4_k_batched:32", "q4_k_batched:64", "moe:1", "moe:16"]
