@@ -197,8 +197,33 @@ int matmul_dev(g4_ctx *ctx, const g4_weight *w, int64_t off, const float *d_x, f
   return launch_status(g4::launch_rows(w->type, g4::EPI_STORE, a, 1, ctx->dev, nullptr, ctx->stream), "matmul");
 }
 
+g4::TokArgs tok_args(const g4_weight *w, int64_t off, const float *d_X, int32_t M, float *d_Y, int32_t dim0,
+                     int32_t dim1) {
+  g4::TokArgs t;
+  t.W = w->d;
+  t.base = off;
+  t.row_stride = dim1;
+  t.rows = dim0;
+  t.dim1 = dim1;
+  t.x = d_X;
+  t.x_stride = dim1;
+  t.M = M;
+  t.y = d_Y;
+  t.y_stride = dim0;
+  t.part = nullptr;
+  return t;
+}
+
+// Scratch floats batch_dev needs for partial sums (carved by the caller).
+int64_t batch_part_floats(const g4_ctx *ctx, const g4_weight *w, int64_t off, int32_t M, int32_t dim0,
+                          int32_t dim1) {
+  if (M < 2 || dim0 == 0 || dim1 == 0) return 0;
+  const g4::TokArgs t = tok_args(w, off, nullptr, M, nullptr, dim0, dim1);
+  return g4::tok_ok(w->type, t) ? g4::tok_scratch_floats(t, ctx->dev) : 0;
+}
+
 int batch_dev(g4_ctx *ctx, const g4_weight *w, int64_t off, const float *d_X, int32_t M, float *d_Y, int32_t dim0,
-              int32_t dim1) {
+              int32_t dim1, float *d_part) {
   if (dim0 == 0 || M == 0) return G4_OK;
   if (dim1 == 0) {
     G4_HIP(hipMemsetAsync(d_Y, 0, sizeof(float) * (size_t)dim0 * M, ctx->stream), "hipMemsetAsync");
@@ -206,19 +231,11 @@ int batch_dev(g4_ctx *ctx, const g4_weight *w, int64_t off, const float *d_X, in
   }
   // several tokens: the matrix-core kernel unpacks each weight once for all of them
   if (M >= 2) {
-    g4::TokArgs t;
-    t.W = w->d;
-    t.base = off;
-    t.row_stride = dim1;
-    t.rows = dim0;
-    t.dim1 = dim1;
-    t.x = d_X;
-    t.x_stride = dim1;
-    t.M = M;
-    t.y = d_Y;
-    t.y_stride = dim0;
-    if (g4::tok_ok(w->type, t))
+    g4::TokArgs t = tok_args(w, off, d_X, M, d_Y, dim0, dim1);
+    if (g4::tok_ok(w->type, t)) {
+      t.part = d_part;
       return launch_status(g4::launch_tok(w->type, t, ctx->dev, ctx->stream), "matmul_batch");
+    }
   }
   g4::RowsArgs a = plain_rows(w, off, d_X, d_Y, dim0, dim1);
   a.x_stride = dim1;
@@ -567,10 +584,11 @@ int g4_matmul_batch(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const 
   G4_TRY(use_device(ctx));
   Carve c;
   size_t ox = c.add(sizeof(float) * (size_t)dim1 * M), oy = c.add(sizeof(float) * (size_t)dim0 * M);
+  size_t op = c.add(sizeof(float) * (size_t)batch_part_floats(ctx, w, this_offset, M, dim0, dim1));
   G4_TRY(ensure_scratch(ctx, c.off));
-  float *dx = (float *)(ctx->scratch + ox), *dy = (float *)(ctx->scratch + oy);
+  float *dx = (float *)(ctx->scratch + ox), *dy = (float *)(ctx->scratch + oy), *dp = (float *)(ctx->scratch + op);
   G4_TRY(copy_in(ctx, dx, X, sizeof(float) * (size_t)dim1 * M));
-  G4_TRY(batch_dev(ctx, w, this_offset, dx, M, dy, dim0, dim1));
+  G4_TRY(batch_dev(ctx, w, this_offset, dx, M, dy, dim0, dim1, dp));
   G4_TRY(copy_out(ctx, Y, dy, sizeof(float) * (size_t)dim0 * M));
   return finish(ctx);
 }
@@ -585,7 +603,9 @@ int g4_matmul_batch_dev(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, co
   if ((!d_X && M > 0 && dim1 > 0) || (!d_Y && M > 0 && dim0 > 0))
     return fail(G4_ERR_INVALID_ARGUMENT, "X/Y is null");
   G4_TRY(use_device(ctx));
-  return batch_dev(ctx, w, this_offset, d_X, M, d_Y, dim0, dim1);
+  const int64_t pf = batch_part_floats(ctx, w, this_offset, M, dim0, dim1);
+  if (pf > 0) G4_TRY(ensure_scratch(ctx, sizeof(float) * (size_t)pf));
+  return batch_dev(ctx, w, this_offset, d_X, M, d_Y, dim0, dim1, pf > 0 ? (float *)ctx->scratch : nullptr);
 }
 
 // -------------------------------------------------------------- argmax ----

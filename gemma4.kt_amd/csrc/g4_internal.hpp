@@ -65,10 +65,13 @@ struct TokArgs {
   int32_t M;
   float *y;
   int64_t y_stride;
+  float *part;  // tok_scratch_floats() floats of column-split partial sums (null when that is 0)
 };
 
 // True when (type, offsets, dim1) take the matrix-core kernel (Q4_K, 64-element aligned rows).
 bool tok_ok(int type, const TokArgs &a);
+// Scratch the launch needs for partial sums (0: one column split, y written directly).
+int64_t tok_scratch_floats(const TokArgs &a, const DevInfo &dev);
 hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_t stream);
 
 hipError_t launch_dequant(int type, const uint8_t *W, int64_t offset, int64_t n, float *out, hipStream_t stream);

@@ -331,8 +331,12 @@ __global__ __launch_bounds__(64) void k_route(const float *logits, int32_t E, in
   __shared__ float p[ROUTE_MAX_E];
   __shared__ float pick_w[ROUTE_MAX_E];
   __shared__ int32_t pick_i[ROUTE_MAX_E];
+  __shared__ float es[ROUTE_MAX_E];
   const int t = blockIdx.x, lane = threadIdx.x;
   const float *lg = logits + (int64_t)t * E;
+  // the expert scales come in with the logits (not in a dependent load at the end)
+  if (expert_scale)
+    for (int i = lane; i < E; i += 64) es[i] = expert_scale[i];
   float m = -__builtin_inff();
   for (int i = lane; i < E; i += 64) m = java_max(m, lg[i]);
 #pragma unroll
@@ -370,7 +374,7 @@ __global__ __launch_bounds__(64) void k_route(const float *logits, int32_t E, in
     const int id = pick_i[j];
     float w = pick_w[j];
     if (renorm) w = __fdiv_rn(w, renorm_sum);
-    if (expert_scale) w = __fmul_rn(w, expert_scale[id]);
+    if (expert_scale) w = __fmul_rn(w, es[id]);
     ids[(int64_t)t * K + j] = id;
     weights[(int64_t)t * K + j] = w;
   }

@@ -17,11 +17,16 @@
 // columns), B = weight nibbles (32 columns x 16 rows), C = 16 tokens x 16 rows:
 // lane l holds A row l%16 / B column l%16 at columns 8(l/16)..+8, and C column
 // l%16 (a weight row) at tokens 4(l/16)..+4, so the lane that unpacks weight row
-// n also owns that row's outputs and scales.  A workgroup is 8 waves; in each
-// column pass (2048 columns) wave w owns columns [256 w, 256 w + 256) and keeps
-// that slice of x, split into bf16 parts, in registers while the workgroup
-// walks its 16-row tiles.  The 8 per-wave partial tiles are summed in wave
-// order through LDS (deterministic), then stored (later passes add to y).
+// n also owns that row's outputs and scales.  A workgroup is 8 waves.  Each
+// wave keeps 4 (token tile, 64-column group) pairs of x split into bf16 parts
+// in registers -- 4 groups of one token tile, 2 groups of 2 or 1 group of 4 --
+// and walks the workgroup's 16-row tiles, unpacking each weight once for its
+// token tiles.  The 8 per-wave partial tiles are summed in wave order through
+// LDS (deterministic).  When the columns need more than one workgroup (more
+// than 8 x 4 / TT groups) the column splits store partial sums that
+// k_tok_reduce adds in split order.  Splitting the columns this way keeps the x
+// each workgroup loads and splits to its own share, so the split work does not
+// grow with the number of workgroups.
 #include "g4_device.hpp"
 #include "g4_internal.hpp"
 
@@ -31,9 +36,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
 
-constexpr int TOK_WAVES = 8;                   // column slices per workgroup
-constexpr int TOK_GPW = 4;                     // 64-column groups per wave per pass
-constexpr int TOK_PASS = TOK_WAVES * TOK_GPW;  // groups per pass (2048 columns)
+constexpr int TOK_WAVES = 8;  // column slices (waves) per workgroup
+constexpr int TOK_SLOTS = 4;  // (token tile, 64-column group) pairs a wave keeps split in registers
 
 // x = p1 + p2 + p3 exactly (each residual is exact in fp32; the third has at
 // most 8 significant bits).  Infinite or NaN x stay in p1 with zero residuals.
@@ -63,169 +67,215 @@ G4_DEV bf16x8 nibbles_bf16(uint32_t w0, uint32_t w1) {
   return r;
 }
 
-template <bool MULTI>
+// TT token tiles per wave and GPW = TOK_SLOTS / TT column groups per wave: a
+// workgroup covers TOK_WAVES * GPW groups (its column split, blockIdx.y) for TT
+// token tiles (token group blockIdx.z) over a range of 16-row tiles
+// (blockIdx.x).  A wave unpacks each weight once for its TT token tiles.
+template <int TT>
 __global__ __launch_bounds__(512) void k_tok_q4k(TokArgs a) {
-  __shared__ f32x4 red[2][TOK_WAVES][64];
+  constexpr int GPW = TOK_SLOTS / TT;
+  __shared__ f32x4 red[2][TT][TOK_WAVES][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, j = lane >> 4;
-  const int tt = blockIdx.y;
-  const int tok = tt * 16 + n;  // A row (token) of this lane
-  const bool tok_ok = tok < a.M;
-  const float *xt = a.x + (int64_t)(tok_ok ? tok : 0) * a.x_stride;
   const int C = a.dim1 >> 6;
-  const int passes = MULTI ? (C + TOK_PASS - 1) / TOK_PASS : 1;
+  const int g0 = ((int)blockIdx.y * TOK_WAVES + wid) * GPW;  // first group of this wave's slice
+  const int ng = max(0, min(GPW, C - g0));                   // wave-uniform
+  const int tt0 = (int)blockIdx.z * TT;                      // first token tile
   const int n_rt = (a.rows + 15) >> 4;
   const int rpb = (n_rt + gridDim.x - 1) / gridDim.x;
   const int rt0 = min(n_rt, (int)blockIdx.x * rpb), rt1 = min(n_rt, rt0 + rpb);
+  // one column split: y directly; several: this split's partial sums
+  float *out = gridDim.y == 1 ? a.y : a.part + (int64_t)blockIdx.y * a.M * a.rows;
+  const int64_t out_stride = gridDim.y == 1 ? a.y_stride : a.rows;
   int buf = 0;
 
-  for (int pass = 0; pass < passes; ++pass) {
-    const int g0 = pass * TOK_PASS + wid * TOK_GPW;  // first group of this wave's slice
-    const int ng = max(0, min(TOK_GPW, C - g0));     // wave-uniform
-
-    // weight group gi of row tile rt, this lane's row (B column n) and K-slice j:
-    // 8 nibble bytes at qs[32 g + 8 j] and the super-block head
-    auto load_w = [&](int rt, bool live, u32x2a4 (&Q)[TOK_GPW], u32x4 (&H)[TOK_GPW], int (&gs)[TOK_GPW]) {
-      const int r = rt * 16 + n;
-      const bool rok = live && r < a.rows;
+  // weight group gi of row tile rt, this lane's row (B column n) and K-slice j:
+  // 8 nibble bytes at qs[32 g + 8 j] and the super-block head
+  auto load_w = [&](int rt, bool live, u32x2a4 (&Q)[GPW], u32x4 (&H)[GPW], int (&gs)[GPW]) {
+    const int r = rt * 16 + n;
+    const bool rok = live && r < a.rows;
 #pragma unroll
-      for (int gi = 0; gi < TOK_GPW; ++gi) {
-        // rows past the end and groups past the slice read the first group of
-        // the tensor (in bounds; never stored / never multiplied)
-        const int64_t e = (rok && gi < ng) ? a.base + (int64_t)r * a.row_stride + (int64_t)(g0 + gi) * 64 : 0;
-        const int64_t G = e >> 6;
-        const uint8_t *sb = a.W + (G >> 2) * 144;
-        gs[gi] = (int)(G & 3);
-        H[gi] = *(const u32x4 *)sb;
-        Q[gi] = *(const u32x2a4 *)(sb + 16 + 32 * (G & 3) + 8 * j);
-      }
-    };
+    for (int gi = 0; gi < GPW; ++gi) {
+      // rows past the end and groups past the slice read the first group of
+      // the tensor (in bounds; never stored / never multiplied)
+      const int64_t e = (rok && gi < ng) ? a.base + (int64_t)r * a.row_stride + (int64_t)(g0 + gi) * 64 : 0;
+      const int64_t G = e >> 6;
+      const uint8_t *sb = a.W + (G >> 2) * 144;
+      gs[gi] = (int)(G & 3);
+      H[gi] = *(const u32x4 *)sb;
+      Q[gi] = *(const u32x2a4 *)(sb + 16 + 32 * (G & 3) + 8 * j);
+    }
+  };
 
-    // x slice: token tok, columns 64 g + 32 h + 8 j .. +8 for g in the slice
-    u32x4a4 xr[TOK_GPW][2][2];
+  // x slice: token (tt0 + ti) * 16 + n, columns 64 g + 32 h + 8 j .. +8
+  u32x4a4 xr[TT][GPW][2][2];
+  bool tok_ok[TT];
 #pragma unroll
-    for (int gi = 0; gi < TOK_GPW; ++gi)
+  for (int ti = 0; ti < TT; ++ti) {
+    const int tok = (tt0 + ti) * 16 + n;
+    tok_ok[ti] = tok < a.M;
+    const float *xt = a.x + (int64_t)(tok_ok[ti] ? tok : 0) * a.x_stride;
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int g = gi < ng ? g0 + gi : 0;
         const u32x4a4 *p = (const u32x4a4 *)(xt + (int64_t)g * 64 + 32 * h + 8 * j);
-        xr[gi][h][0] = p[0];
-        xr[gi][h][1] = p[1];
+        xr[ti][gi][h][0] = p[0];
+        xr[ti][gi][h][1] = p[1];
       }
+  }
 
-    u32x2a4 QA[TOK_GPW], QB[TOK_GPW];
-    u32x4 HA[TOK_GPW], HB[TOK_GPW];
-    int GA[TOK_GPW], GB[TOK_GPW];
-    // the first tile's weight loads go out behind the x loads and before any
-    // use of x (vmcnt retires in order: the split below waits for x only)
-    __builtin_amdgcn_sched_barrier(0);
-    load_w(rt0, rt0 < rt1, QA, HA, GA);
-    __builtin_amdgcn_sched_barrier(0);
+  u32x2a4 QA[GPW], QB[GPW];
+  u32x4 HA[GPW], HB[GPW];
+  int GA[GPW], GB[GPW];
+  // the first tile's weight loads go out behind the x loads and before any
+  // use of x (vmcnt retires in order: the split below waits for x only)
+  __builtin_amdgcn_sched_barrier(0);
+  load_w(rt0, rt0 < rt1, QA, HA, GA);
+  __builtin_amdgcn_sched_barrier(0);
 
-    float xv[TOK_GPW][2][8];
+  // bf16 parts (A operands) and per-sub-block sums of x, the latter on the
+  // matrix cores as parts x ones: the result lands in the C layout (token
+  // 4 j + i of the tile, any column), fp32-accumulated like the products
+  bf16x8 A[TT][GPW][2][3];
+  float xs[TT][GPW][2][4];
+  bf16x8 ones;
 #pragma unroll
-    for (int gi = 0; gi < TOK_GPW; ++gi)
+  for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
+#pragma unroll
+  for (int ti = 0; ti < TT; ++ti)
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const uint32_t m = opaque((tok_ok && gi < ng) ? ~0u : 0u);
+        const uint32_t m = opaque((tok_ok[ti] && gi < ng) ? ~0u : 0u);
+        float v[8];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          xv[gi][h][4 * u] = __uint_as_float(xr[gi][h][u].x & m);
-          xv[gi][h][4 * u + 1] = __uint_as_float(xr[gi][h][u].y & m);
-          xv[gi][h][4 * u + 2] = __uint_as_float(xr[gi][h][u].z & m);
-          xv[gi][h][4 * u + 3] = __uint_as_float(xr[gi][h][u].w & m);
+          v[4 * u] = __uint_as_float(xr[ti][gi][h][u].x & m);
+          v[4 * u + 1] = __uint_as_float(xr[ti][gi][h][u].y & m);
+          v[4 * u + 2] = __uint_as_float(xr[ti][gi][h][u].z & m);
+          v[4 * u + 3] = __uint_as_float(xr[ti][gi][h][u].w & m);
         }
-      }
-
-    // bf16 parts (A operands) and per-sub-block sums of x, the latter on the
-    // matrix cores as parts x ones: the result lands in the C layout (token
-    // 4 j + i of the tile, any column), fp32-accumulated like the products
-    bf16x8 A[TOK_GPW][2][3];
-    float xs[TOK_GPW][2][4];
-    bf16x8 ones;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
-#pragma unroll
-    for (int gi = 0; gi < TOK_GPW; ++gi)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        split3(xv[gi][h], A[gi][h][0], A[gi][h][1], A[gi][h][2]);
+        split3(v, A[ti][gi][h][0], A[ti][gi][h][1], A[ti][gi][h][2]);
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int p = 0; p < 3; ++p) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[gi][h][p], ones, s, 0, 0, 0);
+        for (int p = 0; p < 3; ++p) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[ti][gi][h][p], ones, s, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xs[gi][h][i] = s[i];
+        for (int i = 0; i < 4; ++i) xs[ti][gi][h][i] = s[i];
       }
 
-    auto tile = [&](int rt, const u32x2a4 (&Q)[TOK_GPW], const u32x4 (&H)[TOK_GPW], const int (&gs)[TOK_GPW]) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  auto tile = [&](int rt, const u32x2a4 (&Q)[GPW], const u32x4 (&H)[GPW], const int (&gs)[GPW]) {
+    f32x4 acc[TT];
 #pragma unroll
-      for (int gi = 0; gi < TOK_GPW; ++gi) {
-        if (gi < ng) {  // wave-uniform
-          const uint32_t w0 = Q[gi].x, w1 = Q[gi].y;
-          const bf16x8 bl = nibbles_bf16(opaque(w0 & 0x0F0F0F0Fu), opaque(w1 & 0x0F0F0F0Fu));
-          const bf16x8 bh = nibbles_bf16(opaque(w0 & 0xF0F0F0F0u), opaque(w1 & 0xF0F0F0F0u));
-          // getScaleMinK4 (Q4_KFloatTensor.kt:70-84) for sub-blocks 2g, 2g+1 of
-          // this lane's row: bytes 2(g&1), 2(g&1)+1 of the three scale dwords
-          const int g = gs[gi];
-          const uint32_t sh = (uint32_t)(g & 1) * 16u;
-          const uint32_t y = H[gi].y >> sh, z = H[gi].z >> sh, w = H[gi].w >> sh;
-          const uint32_t scp = g < 2 ? (y & 0x3F3Fu) : ((w & 0x0F0Fu) | ((y >> 2) & 0x3030u));
-          const uint32_t mp = g < 2 ? (z & 0x3F3Fu) : (((w >> 4) & 0x0F0Fu) | ((z >> 2) & 0x3030u));
-          const float d = h2f(H[gi].x & 0xFFFFu), dmin = h2f(H[gi].x >> 16);
-          const float d1 = d * ubyte(scp, 0), d2 = d * ubyte(scp, 1) * 0.0625f;
-          const float m1 = dmin * ubyte(mp, 0), m2 = dmin * ubyte(mp, 1);
-          f32x4 pl = {0.f, 0.f, 0.f, 0.f}, ph = {0.f, 0.f, 0.f, 0.f};
+    for (int ti = 0; ti < TT; ++ti) acc[ti] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int p = 0; p < 3; ++p) {
-            pl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[gi][0][p], bl, pl, 0, 0, 0);
-            ph = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[gi][1][p], bh, ph, 0, 0, 0);
+    for (int gi = 0; gi < GPW; ++gi) {
+      if (gi < ng) {  // wave-uniform
+        const uint32_t w0 = Q[gi].x, w1 = Q[gi].y;
+        const bf16x8 bl = nibbles_bf16(opaque(w0 & 0x0F0F0F0Fu), opaque(w1 & 0x0F0F0F0Fu));
+        const bf16x8 bh = nibbles_bf16(opaque(w0 & 0xF0F0F0F0u), opaque(w1 & 0xF0F0F0F0u));
+        // getScaleMinK4 (Q4_KFloatTensor.kt:70-84) for sub-blocks 2g, 2g+1 of
+        // this lane's row: bytes 2(g&1), 2(g&1)+1 of the three scale dwords
+        const int g = gs[gi];
+        const uint32_t sh = (uint32_t)(g & 1) * 16u;
+        const uint32_t y = H[gi].y >> sh, z = H[gi].z >> sh, w = H[gi].w >> sh;
+        const uint32_t scp = g < 2 ? (y & 0x3F3Fu) : ((w & 0x0F0Fu) | ((y >> 2) & 0x3030u));
+        const uint32_t mp = g < 2 ? (z & 0x3F3Fu) : (((w >> 4) & 0x0F0Fu) | ((z >> 2) & 0x3030u));
+        const float d = h2f(H[gi].x & 0xFFFFu), dmin = h2f(H[gi].x >> 16);
+        const float d1 = d * ubyte(scp, 0), d2 = d * ubyte(scp, 1) * 0.0625f;
+        const float m1 = dmin * ubyte(mp, 0), m2 = dmin * ubyte(mp, 1);
+        // every token tile's products first, then the scale epilogues: the
+        // matrix core works through the independent chains while they drain
+        f32x4 pl[TT], ph[TT];
+#pragma unroll
+        for (int ti = 0; ti < TT; ++ti) pl[ti] = ph[ti] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+          for (int ti = 0; ti < TT; ++ti) {
+            pl[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[ti][gi][0][p], bl, pl[ti], 0, 0, 0);
+            ph[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[ti][gi][1][p], bh, ph[ti], 0, 0, 0);
           }
+#pragma unroll
+        for (int ti = 0; ti < TT; ++ti)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            float v = __builtin_fmaf(d1, pl[i], -(m1 * xs[gi][0][i]));
-            acc[i] += __builtin_fmaf(d2, ph[i], __builtin_fmaf(-m2, xs[gi][1][i], v));
+            acc[ti][i] = __builtin_fmaf(d1, pl[ti][i], acc[ti][i]);
+            acc[ti][i] = __builtin_fmaf(d2, ph[ti][i], acc[ti][i]);
+            acc[ti][i] = __builtin_fmaf(-m1, xs[ti][gi][0][i], acc[ti][i]);
+            acc[ti][i] = __builtin_fmaf(-m2, xs[ti][gi][1][i], acc[ti][i]);
           }
-        }
       }
-      red[buf][wid][lane] = acc;
-      __syncthreads();
-      if (wid == 0) {
-        f32x4 s = red[buf][0][lane];
-#pragma unroll
-        for (int w = 1; w < TOK_WAVES; ++w) s += red[buf][w][lane];
-        const int r = rt * 16 + n;
-        if (r < a.rows) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int m = tt * 16 + 4 * j + i;
-            if (m < a.M) {
-              float *yp = a.y + (int64_t)m * a.y_stride + r;
-              float v = s[i];
-              if constexpr (MULTI) {
-                if (pass > 0) v += *yp;
-              }
-              *yp = v;
-            }
-          }
-        }
-      }
-      buf ^= 1;
-    };
-
-    // two row tiles in flight: tile t+1 loads while tile t multiplies
-    for (int rt = rt0; rt < rt1; rt += 2) {
-      load_w(rt + 1, rt + 1 < rt1, QB, HB, GB);
-      __builtin_amdgcn_sched_barrier(0);
-      tile(rt, QA, HA, GA);
-      __builtin_amdgcn_sched_barrier(0);
-      load_w(rt + 2, rt + 2 < rt1, QA, HA, GA);
-      __builtin_amdgcn_sched_barrier(0);
-      if (rt + 1 < rt1) tile(rt + 1, QB, HB, GB);
-      __builtin_amdgcn_sched_barrier(0);
     }
+    // the TOK_WAVES column slices are summed in wave order (deterministic),
+    // the work spread over the waves: wave w takes token tile w / (8 / TT)'s
+    // components i = c, c + 8/TT, ... of every lane's 4 outputs (c = w % (8/TT))
+#pragma unroll
+    for (int ti = 0; ti < TT; ++ti) red[buf][ti][wid][lane] = acc[ti];
+    __syncthreads();
+    {
+      constexpr int WPT = TOK_WAVES / TT;  // waves per token tile
+      const int ti = wid / WPT, c = wid % WPT;
+      const int r = rt * 16 + n;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (i % WPT == c) {  // wave-uniform
+          float s = red[buf][ti][0][lane][i];
+#pragma unroll
+          for (int w = 1; w < TOK_WAVES; ++w) s += red[buf][ti][w][lane][i];
+          const int m = (tt0 + ti) * 16 + 4 * j + i;
+          if (r < a.rows && m < a.M) out[(int64_t)m * out_stride + r] = s;
+        }
+      }
+    }
+    buf ^= 1;
+  };
+
+  // two row tiles in flight: tile t+1 loads while tile t multiplies
+  for (int rt = rt0; rt < rt1; rt += 2) {
+    load_w(rt + 1, rt + 1 < rt1, QB, HB, GB);
+    __builtin_amdgcn_sched_barrier(0);
+    tile(rt, QA, HA, GA);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(rt + 2, rt + 2 < rt1, QA, HA, GA);
+    __builtin_amdgcn_sched_barrier(0);
+    if (rt + 1 < rt1) tile(rt + 1, QB, HB, GB);
+    __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// y[m * y_stride + r] = sum over the column splits, in split order, of their partial sums.
+__global__ void k_tok_reduce(const float *part, int splits, int32_t M, int32_t rows, float *y, int64_t y_stride) {
+  const int64_t n = (int64_t)M * rows;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    float s = part[i];
+    for (int k = 1; k < splits; ++k) s += part[(int64_t)k * n + i];
+    y[(i / rows) * y_stride + i % rows] = s;
+  }
+}
+
+struct TokShape {
+  int tt, splits, tgroups, gx;
+};
+
+static TokShape tok_shape(const TokArgs &a, const DevInfo &dev) {
+  TokShape sh;
+  const int C = a.dim1 / 64;
+  const int ntt = (a.M + 15) / 16;
+  sh.tt = ntt >= 4 ? 4 : (ntt >= 2 ? 2 : 1);
+  const int gps = TOK_WAVES * (TOK_SLOTS / sh.tt);  // groups per column split
+  sh.splits = (C + gps - 1) / gps;
+  sh.tgroups = (ntt + sh.tt - 1) / sh.tt;
+  // one 8-wave workgroup per CU at a time, spread over every (split, token group)
+  const int n_rt = (a.rows + 15) / 16;
+  int64_t gx = (int64_t)dev.cu_count / ((int64_t)sh.splits * sh.tgroups);
+  if (gx > n_rt) gx = n_rt;
+  if (gx < 1) gx = 1;
+  sh.gx = (int)gx;
+  return sh;
 }
 
 bool tok_ok(int type, const TokArgs &a) {
@@ -235,21 +285,30 @@ bool tok_ok(int type, const TokArgs &a) {
   return a.M >= 1 && a.rows >= 1;
 }
 
+int64_t tok_scratch_floats(const TokArgs &a, const DevInfo &dev) {
+  const TokShape sh = tok_shape(a, dev);
+  return sh.splits > 1 ? (int64_t)sh.splits * a.M * a.rows : 0;
+}
+
 hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_t s) {
   if (!tok_ok(type, a)) return hipErrorInvalidValue;
-  const int C = a.dim1 / 64;
-  const bool multi = C > TOK_PASS;
-  const int n_tt = (a.M + 15) / 16;
-  const int n_rt = (a.rows + 15) / 16;
-  // one 8-wave workgroup per CU at a time: spread the row tiles of every token
-  // tile over cu / n_tt workgroups (each walks its tiles with one in flight)
-  int64_t gx = (dev.cu_count + n_tt - 1) / n_tt;
-  if (gx > n_rt) gx = n_rt;
-  if (gx < 1) gx = 1;
-  if (multi)
-    hipLaunchKernelGGL(k_tok_q4k<true>, dim3((unsigned)gx, (unsigned)n_tt), dim3(512), 0, s, a);
+  const TokShape sh = tok_shape(a, dev);
+  if (sh.splits > 1 && !a.part) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)sh.gx, (unsigned)sh.splits, (unsigned)sh.tgroups);
+  if (sh.tt == 4)
+    hipLaunchKernelGGL(k_tok_q4k<4>, grid, dim3(512), 0, s, a);
+  else if (sh.tt == 2)
+    hipLaunchKernelGGL(k_tok_q4k<2>, grid, dim3(512), 0, s, a);
   else
-    hipLaunchKernelGGL(k_tok_q4k<false>, dim3((unsigned)gx, (unsigned)n_tt), dim3(512), 0, s, a);
+    hipLaunchKernelGGL(k_tok_q4k<1>, grid, dim3(512), 0, s, a);
+  if (sh.splits == 1) return hipGetLastError();
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t n = (int64_t)a.M * a.rows;
+  int blocks = (int)((n + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(k_tok_reduce, dim3(blocks), dim3(256), 0, s, (const float *)a.part, sh.splits, a.M, a.rows,
+                     a.y, a.y_stride);
   return hipGetLastError();
 }
 

@@ -254,10 +254,12 @@ def test_q4_k_batched(g4, ctx, oracle, m):
 
 
 # matrix-core multi-token kernel: partial row and token tiles, several column
-# passes (dim1 > 2048), rows that start mid super-block (1408 = 5.5 super-blocks),
-# a row offset, a single 64-column group
+# splits (summed by the reduce launch), rows that start mid super-block
+# (1408 = 5.5 super-blocks), a row offset, a single 64-column group, 1/2/4 token
+# tiles per wave and several token groups (M = 48, 70)
 @pytest.mark.parametrize("m,rows,dim1,off_rows", [
-    (2, 40, 2048, 0), (17, 34, 4224, 0), (5, 34, 1408, 0), (16, 48, 2048, 3), (3, 20, 64, 0)])
+    (2, 40, 2048, 0), (17, 34, 4224, 0), (5, 34, 1408, 0), (16, 48, 2048, 3), (3, 20, 64, 0),
+    (48, 40, 2048, 0), (70, 24, 4096, 1)])
 def test_q4_k_batched_matrix_core_shapes(g4, ctx, oracle, m, rows, dim1, off_rows):
     announce("q4_k batched M=%d rows=%d dim1=%d off_rows=%d" % (m, rows, dim1, off_rows))
     n = (rows + off_rows) * dim1
@@ -310,6 +312,24 @@ def test_moe_q4_k(g4, ctx, oracle, tokens):
     Y = g4.moe(ctx, wgu, wdn, c["x"], ids, gw, D, FF)
     y64, bound = oracle.moe_exact(Q4_K, c["gate_up"], Q4_K, c["down"], c["x"], rids, rw, D, FF)
     assert_dots(Y.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe T=%d" % tokens)
+
+
+def test_moe_repeated_calls(g4, ctx, oracle):
+    """Back-to-back MoE calls on one context with changing token counts: the
+    context's scratch is re-carved per call and nothing leaks from one call to the next."""
+    announce("moe repeated calls")
+    E, D, FF, K = 16, 512, 256, 4
+    gu = synth.q4_k(48, "gu", E * 2 * FF * D)
+    dn = synth.q4_k(48, "dn", E * D * FF)
+    wgu = upload(g4, ctx, Q4_K, gu, E * 2 * FF * D)
+    wdn = upload(g4, ctx, Q4_K, dn, E * D * FF)
+    for call, T in enumerate([3, 16, 1, 16, 40, 2]):
+        lg = synth.activations(48, "lg%d" % call, T * E).reshape(T, E)
+        X = synth.activations(48, "X%d" % call, T * D).reshape(T, D)
+        ids, gw = g4.moe_route(ctx, lg, K, True)
+        Y = g4.moe(ctx, wgu, wdn, X, ids, gw, D, FF)
+        y64, bound = oracle.moe_exact(Q4_K, gu, Q4_K, dn, X, ids, gw, D, FF)
+        assert_dots(Y.reshape(-1), y64.reshape(-1), bound.reshape(-1), "call %d T=%d" % (call, T))
 
 
 def test_moe_reference_gates(g4, ctx, oracle):
