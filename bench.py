@@ -16,7 +16,8 @@ oracle's restatement of the reference's 512-bit Vector API path on the host
 cores over a bounded sample of the same workload.
 
 Other workloads: --workload q8_0_matvec | q4_0_ffn | q8_0_lm_head |
-q4_k_batched[:M] | moe[:T]; --all prints one line per workload.
+q4_k_batched[:M] | moe[:T] | q5_k_matvec | q6_k_matvec; --all prints one line
+per workload.
 """
 from __future__ import annotations
 
@@ -302,6 +303,41 @@ class MoeQ4_K(Workload):
                 "algorithmic_bytes_per_step": self.step_bytes}
 
 
+class MatvecKQuant(Workload):
+    """Single-token matvec of an 8192x2048 Q5_K or Q6_K matrix (the K-quants a
+    llama.cpp mix pairs with Q4_K; no reference configuration, measured for parity
+    of coverage): x ~ N(0,1), y = W x."""
+
+    def __init__(self, g4, ctx, torch, ggml_type):
+        import synth
+        self.t = ggml_type
+        fmt = {13: "q5_k", 14: "q6_k"}[ggml_type]
+        self.name = "%s_matvec_8192x2048" % fmt
+        self.dominant_name = "k_rows<Fmt%s, 32, EPI_STORE>" % fmt.upper()
+        self.R, self.D = 8192, 2048
+        self.raw = synth.weights(0x51A5, fmt, ggml_type, self.R * self.D)
+        self.xh = synth.activations(0x51A5, "x", self.D)
+        self.copies = copies_for(self.raw.nbytes)
+        self.w = [g4.FloatTensorFactory.create(ctx, ggml_type, self.raw, self.R * self.D) for _ in range(self.copies)]
+        self.x = torch.from_numpy(self.xh).cuda()
+        self.y = torch.empty(self.R, dtype=torch.float32, device="cuda")
+        self.step_bytes = self.dominant_bytes = self.raw.nbytes + 4 * (self.D + self.R)
+        self.fmt = fmt
+
+    def step(self, i):
+        self.w[i % self.copies].matmul_dev(self.x, self.y, self.R, self.D)
+
+    def cpu_setup(self, oracle):
+        self.oracle = oracle
+
+    def cpu_step(self):
+        self.oracle.matmul(self.t, self.raw, self.xh, self.R, self.D)
+
+    def config(self):
+        return {"workload": self.name, "format": self.fmt.upper(), "w": [self.R, self.D],
+                "algorithmic_bytes_per_step": self.step_bytes, "weight_copies": self.copies}
+
+
 class CopyCalibration(Workload):
     """A plain fp32 copy of known size (y = x * 1 through torch's elementwise kernel).
 
@@ -339,6 +375,8 @@ def make_workload(spec: str, g4, ctx, torch) -> Workload:
         return BatchedQ4_K(g4, ctx, torch, int(arg or 8))
     if name == "moe":
         return MoeQ4_K(g4, ctx, torch, int(arg or 1))
+    if name in ("q5_k_matvec", "q6_k_matvec"):
+        return MatvecKQuant(g4, ctx, torch, 13 if name == "q5_k_matvec" else 14)
     raise SystemExit("unknown workload %r" % spec)
 
 
@@ -492,7 +530,7 @@ def main():
     specs = args.workload.split(",")
     if args.all:
         specs = ["q4_0_ffn", "q8_0_matvec", "q8_0_lm_head", "q4_k_batched:1", "q4_k_batched:8",
-                 "q4_k_batched:32", "q4_k_batched:64", "moe:1", "moe:16"]
+                 "q4_k_batched:32", "q4_k_batched:64", "moe:1", "moe:16", "q5_k_matvec", "q6_k_matvec"]
     for s in specs:
         line = run(s, args.steps, args.warmup, args.cpu_seconds, not args.eager)
         print(json.dumps(line), flush=True)

@@ -63,7 +63,7 @@ int hip_fail(hipError_t e, const char *what) {
     if (_e != hipSuccess) return hip_fail(_e, what); \
   } while (0)
 
-// GGMLType.kt:16-30 for the supported ids.
+// GGMLType.kt:16-32 for the supported ids.
 bool type_info(int t, int *bs, int *ts) {
   switch (t) {
     case G4_TYPE_F32: *bs = 1; *ts = 4; return true;
@@ -72,6 +72,8 @@ bool type_info(int t, int *bs, int *ts) {
     case G4_TYPE_Q4_0: *bs = 32; *ts = 18; return true;
     case G4_TYPE_Q8_0: *bs = 32; *ts = 34; return true;
     case G4_TYPE_Q4_K: *bs = 256; *ts = 144; return true;
+    case G4_TYPE_Q5_K: *bs = 256; *ts = 176; return true;
+    case G4_TYPE_Q6_K: *bs = 256; *ts = 210; return true;
     default: return false;
   }
 }

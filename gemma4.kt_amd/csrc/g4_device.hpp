@@ -13,7 +13,7 @@
 
 namespace g4 {
 
-enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_BF16 = 30 };
+enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_BF16 = 30 };
 
 // Four dwords at 4-byte alignment: one global_load_dwordx4 (gfx950 needs dword alignment only).
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -58,7 +58,8 @@ G4_DEV int q4k_scale_min(int j, const uint8_t *s, bool is_min) {
 
 // Per-element get(index), bit-exact restatement of the reference:
 // Q8_0FloatTensor.kt:21-28, Q4_0FloatTensor.kt:21-39, Q4_KFloatTensor.kt:23-55,
-// F16FloatTensor.kt:20-23, BF16FloatTensor.kt:20-24, F32FloatTensor.kt:18-20.
+// Q5_KFloatTensor.kt:23-50, Q6_KFloatTensor.kt:26-75, F16FloatTensor.kt:20-23,
+// BF16FloatTensor.kt:20-24, F32FloatTensor.kt:18-20.
 // __fmul_rn/__fsub_rn keep each operation separately rounded like the JVM.
 template <int TYPE>
 G4_DEV float get_elem(const uint8_t *W, int64_t idx) {
@@ -83,6 +84,28 @@ G4_DEV float get_elem(const uint8_t *W, int64_t idx) {
     float d = h2f(rd_u16(b)), dmin = h2f(rd_u16(b + 2));
     float t = __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
     return __fsub_rn(t, __fmul_rn(dmin, (float)m));
+  } else if constexpr (TYPE == T_Q5_K) {
+    const uint8_t *b = W + (idx >> 8) * 176;
+    int within = (int)(idx & 255);
+    int group = within >> 6, high = (within & 63) >= 32 ? 1 : 0, l = within & 31;
+    int sub = group * 2 + high;
+    int sc = q4k_scale_min(sub, b + 4, false);
+    int m = q4k_scale_min(sub, b + 4, true);
+    int byte = b[48 + group * 32 + l];
+    int q = ((high ? (byte >> 4) : byte) & 0xF) | (((b[16 + l] >> sub) & 1) << 4);
+    float d = h2f(rd_u16(b)), dmin = h2f(rd_u16(b + 2));
+    float t = __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
+    return __fsub_rn(t, __fmul_rn(dmin, (float)m));
+  } else if constexpr (TYPE == T_Q6_K) {
+    const uint8_t *b = W + (idx >> 8) * 210;
+    int within = (int)(idx & 255);
+    int half = within >> 7, r = (within & 127) >> 5, l = within & 31;
+    int nib = (b[half * 64 + (r & 1) * 32 + l] >> (4 * (r >> 1))) & 0xF;
+    int hb = (b[128 + half * 32 + l] >> (2 * r)) & 3;
+    int q6 = (nib | (hb << 4)) - 32;
+    int sc = (int8_t)b[192 + half * 8 + r * 2 + (l >> 4)];
+    float d = h2f(rd_u16(b + 208));
+    return __fmul_rn(__fmul_rn(d, (float)sc), (float)q6);
   } else if constexpr (TYPE == T_F16) {
     return h2f(rd_u16(W + idx * 2));
   } else if constexpr (TYPE == T_BF16) {
@@ -109,8 +132,11 @@ G4_DEV float dot_elem(const uint8_t *W, int64_t idx, int j, int dim1) {
 // 64-element chunks.  A chunk starts at an element offset e that is a multiple
 // of 64 and holds: Q8_0 two blocks (68 B), Q4_0 two blocks (36 B), Q4_K one
 // 64-weight group of a super-block (32 B of nibbles + the 16 B super-block
-// head), F16/BF16 128 B, F32 256 B.  load() issues only dword-aligned vector
-// loads; dot() unpacks in registers against x[0..64) and the precomputed sums.
+// head), Q5_K the same plus the 32 B of fifth bits, Q6_K a quarter super-block
+// (64 B of nibbles shared with the neighbouring chunk, 32 B of bit pairs, 4
+// scales, d), F16/BF16 128 B, F32 256 B.  load() issues only dword-aligned
+// vector loads (plus 16-bit ones for Q6_K's scales and d); dot() unpacks in
+// registers against x[0..64) and the precomputed sums.
 // ---------------------------------------------------------------------------
 
 // Q8_0: {fp16 d, int8 q[32]} x 2 = 17 dwords starting dword-aligned (68 * k).
@@ -247,6 +273,130 @@ struct FmtQ4_K {
     const float m1 = dmin * ubyte(mp, 0), m2 = dmin * ubyte(mp, 1);
     float r = __builtin_fmaf(d1, lo, -(m1 * s[0]));
     return __builtin_fmaf(d2, hi, __builtin_fmaf(-m2, s[1], r));
+  }
+};
+
+// Q5_K: super-block {fp16 d, fp16 dmin, scales[12], qh[32], qs[128]} (176 B,
+// 16-byte aligned).  Group g as Q4_K, with the fifth bit of weight l of
+// sub-block s = 2g + h in bit s of qh[l]: q = nibble + 16 bit, w = d*sc*q -
+// dmin*m (Q5_KFloatTensor.kt:23-50).  Per sub-block: d*sc * sum(x q) -
+// dmin*m * sum(x).
+struct FmtQ5_K {
+  static constexpr int TYPE = T_Q5_K, NDW = 20, NS = 2, RT = 2;
+  G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
+    int64_t G = e >> 6;
+    const uint8_t *sb = W + (G >> 2) * 176;
+    const u32x4 *qs = (const u32x4 *)(sb + 48 + 32 * (int)(G & 3));
+    const u32x4 *qh = (const u32x4 *)(sb + 16);
+    u32x4 h = *(const u32x4 *)sb, q0 = qs[0], q1 = qs[1], h0 = qh[0], h1 = qh[1];
+    D[0] = q0.x; D[1] = q0.y; D[2] = q0.z; D[3] = q0.w;
+    D[4] = q1.x; D[5] = q1.y; D[6] = q1.z; D[7] = q1.w;
+    D[8] = h0.x; D[9] = h0.y; D[10] = h0.z; D[11] = h0.w;
+    D[12] = h1.x; D[13] = h1.y; D[14] = h1.z; D[15] = h1.w;
+    D[16] = h.x; D[17] = h.y; D[18] = h.z; D[19] = h.w;
+  }
+  G4_DEV static void sums(const float *x, float *s) { FmtQ4_K::sums(x, s); }
+  G4_DEV static float dot(const uint32_t (&D)[NDW], const float *x, const float *s, int64_t e) {
+    const int g = (int)((e >> 6) & 3);
+    const uint32_t lsh = 2u * (uint32_t)g, hsh = lsh + 1u;
+    float lo = 0.f, hi = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t Q = D[i], H = D[8 + i];
+      const uint32_t l = opaque((Q & 0x0F0F0F0Fu) | (((H >> lsh) & 0x01010101u) << 4));
+      const uint32_t h = opaque(((Q >> 4) & 0x0F0F0F0Fu) | (((H >> hsh) & 0x01010101u) << 4));
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        lo = __builtin_fmaf(x[4 * i + b], ubyte(l, b), lo);
+        hi = __builtin_fmaf(x[32 + 4 * i + b], ubyte(h, b), hi);
+      }
+    }
+    // getScaleMinK4 for sub-blocks 2g, 2g+1 (as FmtQ4_K::dot)
+    const uint32_t sh = (uint32_t)(g & 1) * 16u;
+    const uint32_t y = D[17] >> sh, z = D[18] >> sh, w = D[19] >> sh;
+    uint32_t scp, mp;
+    if (g < 2) {
+      scp = y & 0x3F3Fu;
+      mp = z & 0x3F3Fu;
+    } else {
+      scp = (w & 0x0F0Fu) | ((y >> 2) & 0x3030u);
+      mp = ((w >> 4) & 0x0F0Fu) | ((z >> 2) & 0x3030u);
+    }
+    const float d = h2f(D[16] & 0xFFFFu), dmin = h2f(D[16] >> 16);
+    const float d1 = d * ubyte(scp, 0), d2 = d * ubyte(scp, 1);
+    const float m1 = dmin * ubyte(mp, 0), m2 = dmin * ubyte(mp, 1);
+    float r = __builtin_fmaf(d1, lo, -(m1 * s[0]));
+    return __builtin_fmaf(d2, hi, __builtin_fmaf(-m2, s[1], r));
+  }
+};
+
+// Q6_K: super-block {ql[128], qh[64], int8 scales[16], fp16 d} (210 B, so odd
+// super-blocks start at 2 mod 4).  Chunk c = 2n + p (half n, part p) reads
+// ql[64n .. 64n+64) -- low nibbles for p = 0, high for p = 1; its first 32
+// weights use ql[64n + l], the next 32 ql[64n + 32 + l] -- bit pairs 4p and
+// 4p + 2 of qh[32n + l], and scales[8n + 4p + k] for its k-th 16 weights:
+// w = d*sc*(q - 32) (Q6_KFloatTensor.kt:26-75).  ql and qh come in as
+// dword-aligned loads shifted into place with alignbyte (their windows stay
+// inside the super-block and the one before it); scales and d are read as
+// 16-bit words.  -32 enters through the sums of x over each 16 weights.
+struct FmtQ6_K {
+  static constexpr int TYPE = T_Q6_K, NDW = 29, NS = 4, RT = 2;
+  G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
+    const int64_t sb = e >> 8;
+    const int c = (int)((e >> 6) & 3), n = c >> 1, p = c & 1;
+    const uint8_t *S = W + sb * 210;
+    const u32x4a4 *ql = (const u32x4a4 *)((uintptr_t)(S + 64 * n) & ~(uintptr_t)3);
+    const u32x4a4 *qh = (const u32x4a4 *)((uintptr_t)(S + 128 + 32 * n) & ~(uintptr_t)3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32x4a4 t = ql[i];
+      D[4 * i] = t.x; D[4 * i + 1] = t.y; D[4 * i + 2] = t.z; D[4 * i + 3] = t.w;
+    }
+    D[16] = ((const uint32_t *)ql)[16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      u32x4a4 t = qh[i];
+      D[17 + 4 * i] = t.x; D[18 + 4 * i] = t.y; D[19 + 4 * i] = t.z; D[20 + 4 * i] = t.w;
+    }
+    D[25] = ((const uint32_t *)qh)[8];
+    const uint16_t *sc = (const uint16_t *)(S + 192 + 8 * n + 4 * p);
+    D[26] = sc[0];
+    D[27] = sc[1];
+    D[28] = *(const uint16_t *)(S + 208);
+  }
+  G4_DEV static void sums(const float *x, float *s) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) t += x[16 * k + i];
+      s[k] = t;
+    }
+  }
+  G4_DEV static float dot(const uint32_t (&D)[NDW], const float *x, const float *s, int64_t e) {
+    const uint32_t al = (uint32_t)((e >> 8) & 1) * 2u;  // 210 * sb mod 4
+    const uint32_t p = (uint32_t)((e >> 6) & 1);
+    const uint32_t ns = 4u * p, s0 = 4u * p, s1 = s0 + 2u;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t qa = __builtin_amdgcn_alignbyte(D[i + 1], D[i], al);           // ql[l], l = 4i..4i+3
+      const uint32_t qb = __builtin_amdgcn_alignbyte(D[i + 9], D[i + 8], al);       // ql[32 + l]
+      const uint32_t hv = __builtin_amdgcn_alignbyte(D[18 + i], D[17 + i], al);     // qh[l]
+      const uint32_t va = opaque(((qa >> ns) & 0x0F0F0F0Fu) | (((hv >> s0) & 0x03030303u) << 4));
+      const uint32_t vb = opaque(((qb >> ns) & 0x0F0F0F0Fu) | (((hv >> s1) & 0x03030303u) << 4));
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        acc[i >> 2] = __builtin_fmaf(x[4 * i + b], ubyte(va, b), acc[i >> 2]);
+        acc[2 + (i >> 2)] = __builtin_fmaf(x[32 + 4 * i + b], ubyte(vb, b), acc[2 + (i >> 2)]);
+      }
+    }
+    const uint32_t sc = D[26] | (D[27] << 16);
+    const float d = h2f(D[28]);
+    float r = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r = __builtin_fmaf(d * sbyte(sc, k), __builtin_fmaf(-32.f, s[k], acc[k]), r);
+    return r;
   }
 };
 

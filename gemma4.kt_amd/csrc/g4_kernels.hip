@@ -2,7 +2,8 @@
 //
 // Row-stream matvec engine (k_rows): a wave owns a contiguous range of rows and
 // keeps its 64-column slice of x in registers across them.  Lanes split each
-// row into 64-element chunks (two Q8_0/Q4_0 blocks, one Q4_K group), load them
+// row into 64-element chunks (two Q8_0/Q4_0 blocks, one Q4_K/Q5_K group, a quarter
+// Q6_K super-block), load them
 // with dword-aligned 128-bit loads, unpack in registers and reduce the row
 // partial sums across the lane group with a transposing butterfly.  x is staged
 // once per workgroup in LDS (XOR-swizzled so the per-lane 256-byte reads are
@@ -402,7 +403,8 @@ bool rows_fast_ok(int type, const RowsArgs &a, bool paired) {
   if (paired && (a.dim1 / 64) > 64) return false;  // paired epilogue needs a single column pass
   if (paired && type == T_F32) return false;         // one row step per F32 tile: no room for the pair
   switch (type) {
-    case T_Q8_0: case T_Q4_0: case T_Q4_K: case T_F16: case T_BF16: case T_F32: return true;
+    case T_Q8_0: case T_Q4_0: case T_Q4_K: case T_Q5_K: case T_Q6_K: case T_F16: case T_BF16: case T_F32:
+      return true;
     default: return false;
   }
 }
@@ -491,6 +493,8 @@ static hipError_t launch_generic(int type, const RowsArgs &a, int nmat, int segm
     case T_Q8_0: return launch_generic_t<T_Q8_0>(a, nmat, segments, dev, s);
     case T_Q4_0: return launch_generic_t<T_Q4_0>(a, nmat, segments, dev, s);
     case T_Q4_K: return launch_generic_t<T_Q4_K>(a, nmat, segments, dev, s);
+    case T_Q5_K: return launch_generic_t<T_Q5_K>(a, nmat, segments, dev, s);
+    case T_Q6_K: return launch_generic_t<T_Q6_K>(a, nmat, segments, dev, s);
     case T_F16: return launch_generic_t<T_F16>(a, nmat, segments, dev, s);
     case T_BF16: return launch_generic_t<T_BF16>(a, nmat, segments, dev, s);
     case T_F32: return launch_generic_t<T_F32>(a, nmat, segments, dev, s);
@@ -505,6 +509,8 @@ hipError_t launch_rows(int type, int epi, const RowsArgs &a, int segments, const
       case T_Q8_0: return launch_fast<FmtQ8_0>(epi, a, segments, dev, s);
       case T_Q4_0: return launch_fast<FmtQ4_0>(epi, a, segments, dev, s);
       case T_Q4_K: return launch_fast<FmtQ4_K>(epi, a, segments, dev, s);
+      case T_Q5_K: return launch_fast<FmtQ5_K>(epi, a, segments, dev, s);
+      case T_Q6_K: return launch_fast<FmtQ6_K>(epi, a, segments, dev, s);
       case T_F16: return launch_fast<FmtHalf<T_F16>>(epi, a, segments, dev, s);
       case T_BF16: return launch_fast<FmtHalf<T_BF16>>(epi, a, segments, dev, s);
       case T_F32: return launch_fast<FmtF32>(epi, a, segments, dev, s);
@@ -537,6 +543,8 @@ hipError_t launch_dequant(int type, const uint8_t *W, int64_t offset, int64_t n,
     case T_Q8_0: hipLaunchKernelGGL(k_dequant<T_Q8_0>, dim3(blocks), dim3(256), 0, s, W, offset, n, out); break;
     case T_Q4_0: hipLaunchKernelGGL(k_dequant<T_Q4_0>, dim3(blocks), dim3(256), 0, s, W, offset, n, out); break;
     case T_Q4_K: hipLaunchKernelGGL(k_dequant<T_Q4_K>, dim3(blocks), dim3(256), 0, s, W, offset, n, out); break;
+    case T_Q5_K: hipLaunchKernelGGL(k_dequant<T_Q5_K>, dim3(blocks), dim3(256), 0, s, W, offset, n, out); break;
+    case T_Q6_K: hipLaunchKernelGGL(k_dequant<T_Q6_K>, dim3(blocks), dim3(256), 0, s, W, offset, n, out); break;
     case T_F16: hipLaunchKernelGGL(k_dequant<T_F16>, dim3(blocks), dim3(256), 0, s, W, offset, n, out); break;
     case T_BF16: hipLaunchKernelGGL(k_dequant<T_BF16>, dim3(blocks), dim3(256), 0, s, W, offset, n, out); break;
     case T_F32: hipLaunchKernelGGL(k_dequant<T_F32>, dim3(blocks), dim3(256), 0, s, W, offset, n, out); break;

@@ -157,6 +157,8 @@ class GGMLType(enum.IntEnum):
     Q4_0 = 2
     Q8_0 = 8
     Q4_K = 12
+    Q5_K = 13
+    Q6_K = 14
     BF16 = 30
 
     @property

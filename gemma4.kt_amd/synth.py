@@ -12,12 +12,16 @@ Block layouts written here are the GGUF ones the reference reads:
   Q4_0  18 B / 32 weights : fp16 d, 16 B nibbles        (Q4_0FloatTensor.kt:21-39)
   Q4_K 144 B / 256 weights: fp16 d, fp16 dmin, 12 B packed 6-bit scales/mins,
                             128 B nibbles               (Q4_KFloatTensor.kt:23-84)
+  Q5_K 176 B / 256 weights: as Q4_K plus 32 B of fifth bits before the nibbles
+                                                        (Q5_KFloatTensor.kt:23-50)
+  Q6_K 210 B / 256 weights: 128 B low nibbles, 64 B high bit pairs, int8
+                            scales[16], fp16 d          (Q6_KFloatTensor.kt:26-75)
 """
 from __future__ import annotations
 
 import numpy as np
 
-GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_BF16 = 0, 1, 2, 8, 12, 30
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_BF16 = 0, 1, 2, 8, 12, 13, 14, 30
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
 _M1 = np.uint64(0xBF58476D1CE4E5B9)
@@ -176,6 +180,31 @@ def q4_k(seed: int, tag: str, n_elems: int, dscale: float = 0.01) -> np.ndarray:
     return out.reshape(-1)
 
 
+def q5_k(seed: int, tag: str, n_elems: int, dscale: float = 0.01) -> np.ndarray:
+    """Q5_K super-blocks (176 B): d, dmin = fp16(|N(0,1)| * dscale), 6-bit
+    scales and mins uniform in 0..63 (Q4_K packing), high bits and nibbles uniform."""
+    assert n_elems % 256 == 0
+    nb = n_elems // 256
+    out = np.empty((nb, 176), dtype=np.uint8)
+    out[:, 0:2] = fp16_bits(np.abs(normal(seed, tag + ".d", nb)) * dscale).view(np.uint8).reshape(nb, 2)
+    out[:, 2:4] = fp16_bits(np.abs(normal(seed, tag + ".dmin", nb)) * dscale).view(np.uint8).reshape(nb, 2)
+    sm = random_bytes(seed, tag + ".sm", nb * 16).reshape(nb, 16) & 63
+    out[:, 4:16] = pack_q4k_scales(sm[:, :8], sm[:, 8:])
+    out[:, 16:] = random_bytes(seed, tag + ".q", nb * 160).reshape(nb, 160)
+    return out.reshape(-1)
+
+
+def q6_k(seed: int, tag: str, n_elems: int, dscale: float = 0.002) -> np.ndarray:
+    """Q6_K super-blocks (210 B): 6-bit quants uniform (ql, qh bytes), int8
+    scales uniform in -128..127, d = fp16(|N(0,1)| * dscale) at the end."""
+    assert n_elems % 256 == 0
+    nb = n_elems // 256
+    out = np.empty((nb, 210), dtype=np.uint8)
+    out[:, 0:208] = random_bytes(seed, tag + ".q", nb * 208).reshape(nb, 208)
+    out[:, 208:210] = fp16_bits(np.abs(normal(seed, tag + ".d", nb)) * dscale).view(np.uint8).reshape(nb, 2)
+    return out.reshape(-1)
+
+
 def dense(seed: int, tag: str, n_elems: int, ggml_type: int, scale: float = 0.05) -> np.ndarray:
     v = normal(seed, tag, n_elems) * scale
     if ggml_type == GGML_F32:
@@ -194,6 +223,10 @@ def weights(seed: int, tag: str, ggml_type: int, n_elems: int) -> np.ndarray:
         return q4_0(seed, tag, n_elems)
     if ggml_type == GGML_Q4_K:
         return q4_k(seed, tag, n_elems)
+    if ggml_type == GGML_Q5_K:
+        return q5_k(seed, tag, n_elems)
+    if ggml_type == GGML_Q6_K:
+        return q6_k(seed, tag, n_elems)
     return dense(seed, tag, n_elems, ggml_type)
 
 

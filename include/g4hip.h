@@ -45,6 +45,8 @@ extern "C" {
 #define G4_TYPE_Q4_0 2
 #define G4_TYPE_Q8_0 8
 #define G4_TYPE_Q4_K 12
+#define G4_TYPE_Q5_K 13
+#define G4_TYPE_Q6_K 14
 #define G4_TYPE_BF16 30
 
 typedef struct g4_ctx g4_ctx;

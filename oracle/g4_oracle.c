@@ -35,6 +35,8 @@ int or_block_size(int type) {
     case OR_Q4_0: return 32;
     case OR_Q8_0: return 32;
     case OR_Q4_K: return 256;
+    case OR_Q5_K: return 256;
+    case OR_Q6_K: return 256;
     default: return 0;
   }
 }
@@ -47,6 +49,8 @@ int or_type_size(int type) {
     case OR_Q4_0: return 2 + 16;          /* Float16.BYTES + 16 bytes */
     case OR_Q8_0: return 2 + 32;          /* Float16.BYTES + 32 bytes */
     case OR_Q4_K: return 2 * 2 + 12 + 128; /* 2*Float16.BYTES + 12 + QK_K/2 */
+    case OR_Q5_K: return 2 * 2 + 12 + 32 + 128; /* + QK_K/8 high bits */
+    case OR_Q6_K: return 128 + 64 + 16 + 2;     /* QK_K/2 + QK_K/4 + QK_K/16 + Float16.BYTES */
     default: return 0;
   }
 }
@@ -148,6 +152,52 @@ float or_get(int type, const uint8_t *raw, int64_t index) {
       t = t * (float)quant;
       float u = dmin * (float)m;
       return t - u;
+    }
+    case OR_Q5_K: { /* Q5_KFloatTensor.kt:23-50 */
+      int64_t blk = index / 256;
+      int within = (int)(index % 256);
+      const uint8_t *b = raw + blk * 176;
+      float d = or_fp16_to_f32(rd16(b));
+      float dmin = or_fp16_to_f32(rd16(b + 2));
+      const uint8_t *scales = b + 4, *qh = b + 16, *qs = b + 48;
+      int group = within / 64, in_group = within % 64;
+      int high = in_group >= 32;
+      int l = high ? in_group - 32 : in_group;
+      int sub = group * 2 + high;
+      int sc = or_q4k_scale_min(sub, scales, 0);
+      int m = or_q4k_scale_min(sub, scales, 1);
+      int byte = qs[group * 32 + l];
+      int nibble = high ? ((byte >> 4) & 0xF) : (byte & 0xF);
+      int bit = (qh[l] >> (2 * group + high)) & 1;
+      int quant = nibble | (bit << 4);
+      /* d * sc * quant - dmin * m, left to right in fp32 */
+      float t = d * (float)sc;
+      t = t * (float)quant;
+      float u = dmin * (float)m;
+      return t - u;
+    }
+    case OR_Q6_K: { /* Q6_KFloatTensor.kt:26-75 */
+      int64_t blk = index / 256;
+      int within = (int)(index % 256);
+      const uint8_t *b = raw + blk * 210;
+      const uint8_t *ql = b, *qh = b + 128;
+      const int8_t *scales = (const int8_t *)(b + 192);
+      float d = or_fp16_to_f32(rd16(b + 208));
+      int half = within / 128, rem = within % 128, sub32 = rem / 32, l = rem % 32;
+      const uint8_t *qlb = ql + half * 64, *qhb = qh + half * 32;
+      int nib;
+      switch (sub32) {
+        case 0: nib = qlb[l] & 0xF; break;
+        case 1: nib = qlb[32 + l] & 0xF; break;
+        case 2: nib = (qlb[l] >> 4) & 0xF; break;
+        default: nib = (qlb[32 + l] >> 4) & 0xF; break;
+      }
+      int hb = (qhb[l] >> (2 * sub32)) & 3;
+      int q6 = (nib | (hb << 4)) - 32;
+      int sc = scales[half * 8 + sub32 * 2 + l / 16];
+      /* d * sc * q6, left to right in fp32 */
+      float t = d * (float)sc;
+      return t * (float)q6;
     }
     case OR_F16: /* F16FloatTensor.kt:20-23 */
       return or_fp16_to_f32(rd16(raw + index * 2));
@@ -294,6 +344,97 @@ static float vdot_q4_k(const uint8_t *raw, int64_t off, const float *x, int32_t 
   return result;
 }
 
+/* Q5_KFloatTensor.kt:64-190, 512-bit branch (:125-131): two accumulators, each
+ * element weight fma(q, d*sc, -(dmin*m)) fma'd into its lane. */
+static float vdot_q5_k(const uint8_t *raw, int64_t off, const float *x, int32_t size) {
+  float result = 0.0f;
+  int32_t j = 0;
+  int32_t align = (int32_t)((-off) & 255);
+  if (align > size) align = size;
+  if (align > 0) {
+    result += or_scalar_dot(OR_Q5_K, raw, off, x, align);
+    j += align;
+  }
+  float value[16] = {0}, val2[16] = {0};
+  int64_t block_off = (off + j) / 256 * 176;
+  int32_t upper = j + (size - j) / 256 * 256;
+  while (j < upper) {
+    const uint8_t *b = raw + block_off;
+    float d = or_fp16_to_f32(rd16(b));
+    float dmin = or_fp16_to_f32(rd16(b + 2));
+    const uint8_t *sc = b + 4, *qh = b + 16, *qs = b + 48;
+    for (int g = 0; g < 4; g++) {
+      float d1 = d * (float)or_q4k_scale_min(g * 2, sc, 0);
+      float negM1 = -(dmin * (float)or_q4k_scale_min(g * 2, sc, 1));
+      float d2 = d * (float)or_q4k_scale_min(g * 2 + 1, sc, 0);
+      float negM2 = -(dmin * (float)or_q4k_scale_min(g * 2 + 1, sc, 1));
+      for (int c = 0; c < 2; c++) {
+        const uint8_t *w = qs + g * 32 + c * 16, *hb = qh + c * 16;
+        int32_t lo_base = j + g * 64 + c * 16, hi_base = j + g * 64 + 32 + c * 16;
+        for (int l = 0; l < 16; l++) {
+          float loq = (float)((w[l] & 0xF) | (((hb[l] >> (2 * g)) & 1) << 4));
+          float hiq = (float)((w[l] >> 4) | (((hb[l] >> (2 * g + 1)) & 1) << 4));
+          value[l] = fmaf(fmaf(loq, d1, negM1), x[lo_base + l], value[l]);
+          val2[l] = fmaf(fmaf(hiq, d2, negM2), x[hi_base + l], val2[l]);
+        }
+      }
+    }
+    j += 256;
+    block_off += 176;
+  }
+  float sum[16];
+  for (int l = 0; l < 16; l++) sum[l] = value[l] + val2[l];
+  result += reduce16(sum);
+  if (j < size) result += or_scalar_dot(OR_Q5_K, raw, off + j, x + j, size - j);
+  return result;
+}
+
+/* Q6_KFloatTensor.kt:110-250, 512-bit branch (:196-205): per half and 16-lane
+ * column c, four 6-bit groups q0..q3 (ql low/high nibbles, qh bit pairs), each
+ * weight (float)q * (d*sc) fma'd into one accumulator in q0, q1, q2, q3 order. */
+static float vdot_q6_k(const uint8_t *raw, int64_t off, const float *x, int32_t size) {
+  float result = 0.0f;
+  int32_t j = 0;
+  int32_t align = (int32_t)((-off) & 255);
+  if (align > size) align = size;
+  if (align > 0) {
+    result += or_scalar_dot(OR_Q6_K, raw, off, x, align);
+    j += align;
+  }
+  float acc[16] = {0};
+  int64_t block_off = (off + j) / 256 * 210;
+  int32_t upper = j + (size - j) / 256 * 256;
+  while (j < upper) {
+    const uint8_t *b = raw + block_off;
+    const int8_t *sc = (const int8_t *)(b + 192);
+    float d = or_fp16_to_f32(rd16(b + 208));
+    for (int h = 0; h < 2; h++) {
+      const uint8_t *ql = b + h * 64, *qh = b + 128 + h * 32;
+      int32_t base = j + h * 128;
+      for (int c = 0; c < 2; c++) {
+        float ds0 = d * (float)sc[h * 8 + c], ds1 = d * (float)sc[h * 8 + 2 + c];
+        float ds2 = d * (float)sc[h * 8 + 4 + c], ds3 = d * (float)sc[h * 8 + 6 + c];
+        for (int l = 0; l < 16; l++) {
+          int a = ql[c * 16 + l], bb = ql[32 + c * 16 + l], v = qh[c * 16 + l];
+          int q0 = ((a & 0xF) | ((v & 3) << 4)) - 32;
+          int q1 = ((bb & 0xF) | (((v >> 2) & 3) << 4)) - 32;
+          int q2 = ((a >> 4) | (((v >> 4) & 3) << 4)) - 32;
+          int q3 = ((bb >> 4) | (((v >> 6) & 3) << 4)) - 32;
+          acc[l] = fmaf((float)q0 * ds0, x[base + c * 16 + l], acc[l]);
+          acc[l] = fmaf((float)q1 * ds1, x[base + 32 + c * 16 + l], acc[l]);
+          acc[l] = fmaf((float)q2 * ds2, x[base + 64 + c * 16 + l], acc[l]);
+          acc[l] = fmaf((float)q3 * ds3, x[base + 96 + c * 16 + l], acc[l]);
+        }
+      }
+    }
+    j += 256;
+    block_off += 210;
+  }
+  result += reduce16(acc);
+  if (j < size) result += or_scalar_dot(OR_Q6_K, raw, off + j, x + j, size - j);
+  return result;
+}
+
 /* F16FloatTensor.kt:43-77 / BF16FloatTensor.kt:35-73 / F32FloatTensor.kt:37-65:
  * fma over 16 lanes up to loopBound(size), reduceLanes, scalar tail. */
 static float vdot_dense(int type, const uint8_t *raw, int64_t off, const float *x, int32_t size) {
@@ -322,6 +463,8 @@ float or_vector_dot(int type, const uint8_t *raw, int64_t this_offset, const flo
     case OR_Q8_0: return vdot_q8_0(raw, this_offset, x, size);
     case OR_Q4_0: return vdot_q4_0(raw, this_offset, x, size);
     case OR_Q4_K: return vdot_q4_k(raw, this_offset, x, size);
+    case OR_Q5_K: return vdot_q5_k(raw, this_offset, x, size);
+    case OR_Q6_K: return vdot_q6_k(raw, this_offset, x, size);
     case OR_F16:
     case OR_BF16:
     case OR_F32: return vdot_dense(type, raw, this_offset, x, size);

@@ -26,6 +26,8 @@ enum {
   OR_Q4_0 = 2,
   OR_Q8_0 = 8,
   OR_Q4_K = 12,
+  OR_Q5_K = 13,
+  OR_Q6_K = 14,
   OR_BF16 = 30
 };
 
@@ -54,6 +56,7 @@ void or_fp16_vec_decode_array(const uint16_t *h, int64_t n, float *out);
 
 /* Per-format get(index) (dequantization of one element).
  * Q8_0FloatTensor.kt:21-28, Q4_0FloatTensor.kt:21-39, Q4_KFloatTensor.kt:23-55,
+ * Q5_KFloatTensor.kt:23-50, Q6_KFloatTensor.kt:26-75,
  * F16FloatTensor.kt:20-23, BF16FloatTensor.kt:20-24, F32FloatTensor.kt:18-20. */
 float or_get(int type, const uint8_t *raw, int64_t index);
 void or_dequant(int type, const uint8_t *raw, int64_t offset, int64_t n, float *out);

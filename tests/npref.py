@@ -18,6 +18,17 @@ Layouts (ggml, as read by the reference's *FloatTensor.get):
                      pairs 4..7 keep their low 4 bits in bytes 8..11 (sc low
                      nibble, m high nibble) and their top 2 bits in the top
                      2 bits of bytes 0..3 (sc) and 4..7 (m).
+  Q5_K super-block (176 B): d fp16 | dmin fp16 | scales u8[12] (as Q4_K) |
+                     qh u8[32] | qs u8[128]; group g as Q4_K with the 5th bit
+                     of weight l of sub-block s = 2g + h in bit s of qh[l]:
+                     w = (d*sc)*(nib + 16*bit) - dmin*m.
+  Q6_K super-block (210 B): ql u8[128] | qh u8[64] | scales int8[16] | d fp16;
+                     each 128-weight half n reads ql[64n:64n+64], qh[32n:32n+32],
+                     scales[8n:8n+8]; for l < 32 its four 32-weight rows are
+                     (ql[l] & 15, qh bits 0-1), (ql[l+32] & 15, bits 2-3),
+                     (ql[l] >> 4, bits 4-5), (ql[l+32] >> 4, bits 6-7), the
+                     6-bit value minus 32, row r, lane l scaled by
+                     d * scales[2r + l // 16].
 """
 from __future__ import annotations
 
@@ -72,6 +83,42 @@ def dequant_q4_k(raw: np.ndarray) -> np.ndarray:
     return w.astype(np.float32).reshape(-1)
 
 
+def dequant_q5_k(raw: np.ndarray) -> np.ndarray:
+    sb = raw.reshape(-1, 176)
+    n = sb.shape[0]
+    d = _f16(sb[:, 0:2])
+    dmin = _f16(sb[:, 2:4])
+    sc, m = q4k_unpack_scales(sb[:, 4:16])
+    qh = sb[:, 16:48].astype(np.int32)
+    ql = sb[:, 48:176].reshape(n, 4, 32).astype(np.int32)
+    q = np.empty((n, 4, 2, 32), dtype=np.int32)
+    for g in range(4):
+        q[:, g, 0, :] = (ql[:, g, :] & 0x0F) + 16 * ((qh >> (2 * g)) & 1)
+        q[:, g, 1, :] = (ql[:, g, :] >> 4) + 16 * ((qh >> (2 * g + 1)) & 1)
+    q = q.reshape(n, 8, 32).astype(np.float32)
+    scale = (d[:, None] * sc.astype(np.float32)).astype(np.float32)
+    mins = (dmin[:, None] * m.astype(np.float32)).astype(np.float32)
+    w = (scale[:, :, None] * q).astype(np.float32) - mins[:, :, None]
+    return w.astype(np.float32).reshape(-1)
+
+
+def dequant_q6_k(raw: np.ndarray) -> np.ndarray:
+    sb = raw.reshape(-1, 210)
+    n = sb.shape[0]
+    ql = sb[:, 0:128].reshape(n, 2, 64).astype(np.int32)
+    qh = sb[:, 128:192].reshape(n, 2, 32).astype(np.int32)
+    sc = np.ascontiguousarray(sb[:, 192:208]).view(np.int8).astype(np.float32).reshape(n, 2, 4, 2)
+    d = _f16(sb[:, 208:210])
+    q = np.empty((n, 2, 4, 32), dtype=np.int32)
+    q[:, :, 0, :] = (ql[:, :, 0:32] & 0x0F) | ((qh & 3) << 4)
+    q[:, :, 1, :] = (ql[:, :, 32:64] & 0x0F) | (((qh >> 2) & 3) << 4)
+    q[:, :, 2, :] = (ql[:, :, 0:32] >> 4) | (((qh >> 4) & 3) << 4)
+    q[:, :, 3, :] = (ql[:, :, 32:64] >> 4) | (((qh >> 6) & 3) << 4)
+    ds = (d[:, None, None, None] * sc).astype(np.float32)           # [n, half, row, l // 16]
+    w = np.repeat(ds, 16, axis=3) * (q - 32).astype(np.float32)
+    return w.astype(np.float32).reshape(-1)
+
+
 def dequant_f16(raw: np.ndarray) -> np.ndarray:
     return raw.view(np.float16).astype(np.float32)
 
@@ -87,7 +134,8 @@ def dequant_f32(raw: np.ndarray) -> np.ndarray:
 
 
 def dequant(ggml_type: int, raw: np.ndarray) -> np.ndarray:
-    f = {8: dequant_q8_0, 2: dequant_q4_0, 12: dequant_q4_k, 1: dequant_f16, 30: dequant_bf16, 0: dequant_f32}
+    f = {8: dequant_q8_0, 2: dequant_q4_0, 12: dequant_q4_k, 13: dequant_q5_k, 14: dequant_q6_k, 1: dequant_f16,
+         30: dequant_bf16, 0: dequant_f32}
     return f[ggml_type](np.ascontiguousarray(raw).view(np.uint8).reshape(-1))
 
 

@@ -47,16 +47,19 @@ def test_no_device_here(g4):
 
 
 def test_type_table(g4):
-    # GGMLType.kt:16-30
-    expect = {0: (1, 4), 1: (1, 2), 2: (32, 18), 8: (32, 34), 12: (256, 144), 30: (1, 2)}
+    # GGMLType.kt:16-32
+    expect = {0: (1, 4), 1: (1, 2), 2: (32, 18), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210),
+              30: (1, 2)}
     for t, (bs, ts) in expect.items():
         assert g4.GGMLType(t).block_size == bs and g4.GGMLType(t).type_size == ts
     assert g4.GGMLType.Q8_0.byte_size_for(2048 * 2048) == 4456448
     assert g4.GGMLType.Q4_0.byte_size_for(8192 * 2048) == 9437184
     assert g4.GGMLType.Q4_K.byte_size_for(8192 * 2048) == 9437184
+    assert g4.GGMLType.Q5_K.byte_size_for(8192 * 2048) == 11534336
+    assert g4.GGMLType.Q6_K.byte_size_for(8192 * 2048) == 13762560
 
 
-@pytest.mark.parametrize("bad", [3, 6, 7, 9, 13, 14, 39, 41, -1])
+@pytest.mark.parametrize("bad", [3, 6, 7, 9, 10, 11, 15, 39, 41, -1])
 def test_unsupported_type_ids(g4, bad):
     with pytest.raises(g4.UnsupportedOperationException):
         g4.check_matmul(bad, 1024, 0, 1, 1024)

@@ -15,8 +15,8 @@ from conftest import announce
 
 pytestmark = pytest.mark.gpu
 
-Q8_0, Q4_0, Q4_K, F16, BF16, F32 = 8, 2, 12, 1, 30, 0
-ALL = [Q8_0, Q4_0, Q4_K, F16, BF16, F32]
+Q8_0, Q4_0, Q4_K, Q5_K, Q6_K, F16, BF16, F32 = 8, 2, 12, 13, 14, 1, 30, 0
+ALL = [Q8_0, Q4_0, Q4_K, Q5_K, Q6_K, F16, BF16, F32]
 TOL = 1e-5
 
 
@@ -179,7 +179,7 @@ def test_range_errors_on_device(g4, ctx):
     with pytest.raises(g4.IllegalArgumentException):
         g4.FloatTensorFactory.create(ctx, Q8_0, raw[:100], 64 * 32)
     with pytest.raises(g4.UnsupportedOperationException):
-        g4.FloatTensorFactory.create(ctx, 13, raw, 64 * 32)
+        g4.FloatTensorFactory.create(ctx, 3, raw, 64 * 32)
 
 
 # -------------------------------------------------------------- workloads ---

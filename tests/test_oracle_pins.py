@@ -15,8 +15,8 @@ import torch
 import npref
 import synth
 
-Q8_0, Q4_0, Q4_K, F16, BF16, F32 = 8, 2, 12, 1, 30, 0
-ALL = [Q8_0, Q4_0, Q4_K, F16, BF16, F32]
+Q8_0, Q4_0, Q4_K, Q5_K, Q6_K, F16, BF16, F32 = 8, 2, 12, 13, 14, 1, 30, 0
+ALL = [Q8_0, Q4_0, Q4_K, Q5_K, Q6_K, F16, BF16, F32]
 
 
 def same_bits(a: np.ndarray, b: np.ndarray) -> bool:
@@ -155,10 +155,82 @@ def test_q4k_known_values(oracle, case):
     assert same_bits(oracle.dequant(Q4_K, blk, 0, 256), expect.astype(np.float32))
 
 
+def _q5k_block(d, dmin, sc, m, q5):
+    """Pack a Q5_K super-block from 256 five-bit values (weight e of group g,
+    half h = (e % 64) // 32, lane l: nibble in qs[32g + l], 5th bit in bit 2g + h of qh[l])."""
+    blk = np.zeros(176, np.uint8)
+    blk[0:2] = np.array([d], np.float16).view(np.uint8)
+    blk[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    blk[4:16] = npref.pack_q4k_scales_quantizer(np.array([sc]), np.array([m]))[0]
+    q5 = np.asarray(q5, np.int64)
+    for e in range(256):
+        g, h, l = e // 64, (e % 64) // 32, e % 32
+        blk[48 + 32 * g + l] |= (q5[e] & 15) << (4 * h)
+        blk[16 + l] |= (q5[e] >> 4) << (2 * g + h)
+    return blk
+
+
+@pytest.mark.parametrize("case", ["extremes", "all_high_bits", "random"])
+def test_q5k_known_values(oracle, case):
+    rng = np.random.default_rng(6)
+    if case == "extremes":
+        d, dmin, sc, m = 0.0625, 0.125, [0, 63, 0, 63, 63, 0, 63, 0], [63, 0, 63, 0, 0, 63, 0, 63]
+        q5 = np.tile(np.array([0, 31, 16, 15]), 64)
+    elif case == "all_high_bits":
+        d, dmin, sc, m = 0.5, 0.25, [1, 2, 3, 4, 5, 6, 7, 8], [8, 7, 6, 5, 4, 3, 2, 1]
+        q5 = 16 + rng.integers(0, 16, 256)
+    else:
+        d, dmin = 0.0123, 0.0071
+        sc, m = list(rng.integers(0, 64, 8)), list(rng.integers(0, 64, 8))
+        q5 = rng.integers(0, 32, 256)
+    blk = _q5k_block(d, dmin, sc, m, q5)
+    d32, dm32 = np.float32(np.float16(d)), np.float32(np.float16(dmin))
+    sub = np.repeat(np.arange(8), 32)
+    expect = (d32 * np.array(sc, np.float32)[sub]) * np.asarray(q5, np.float32) - \
+        (dm32 * np.array(m, np.float32)[sub])
+    assert same_bits(oracle.dequant(Q5_K, blk, 0, 256), expect.astype(np.float32))
+    assert same_bits(npref.dequant(Q5_K, blk), expect.astype(np.float32))
+
+
+def _q6k_block(d, scales, q6):
+    """Pack a Q6_K super-block from 256 values in -32..31 (weight e: half n = e // 128,
+    row r = (e % 128) // 32, lane l = e % 32; low nibble in ql[64n + l + 32 (r & 1)]
+    at shift 4 (r >> 1), bit pair at shift 2r of qh[32n + l])."""
+    blk = np.zeros(210, np.uint8)
+    v = np.asarray(q6, np.int64) + 32
+    for e in range(256):
+        n, r, l = e // 128, (e % 128) // 32, e % 32
+        blk[64 * n + l + 32 * (r & 1)] |= (v[e] & 15) << (4 * (r >> 1))
+        blk[128 + 32 * n + l] |= (v[e] >> 4) << (2 * r)
+    blk[192:208] = np.asarray(scales, np.int8).view(np.uint8)
+    blk[208:210] = np.array([d], np.float16).view(np.uint8)
+    return blk
+
+
+@pytest.mark.parametrize("case", ["extremes", "negative_scales", "random"])
+def test_q6k_known_values(oracle, case):
+    rng = np.random.default_rng(9)
+    if case == "extremes":
+        d, scales = 0.5, [127, -128, 1, -1, 0, 64, -64, 2] * 2
+        q6 = np.tile(np.array([-32, 31, 0, -1]), 64)
+    elif case == "negative_scales":
+        d, scales = 2.0 ** -10, list(-np.arange(1, 17) * 8)
+        q6 = rng.integers(-32, 32, 256)
+    else:
+        d, scales = 0.0123, list(rng.integers(-128, 128, 16))
+        q6 = rng.integers(-32, 32, 256)
+    blk = _q6k_block(d, scales, q6)
+    d32 = np.float32(np.float16(d))
+    sidx = (np.arange(256) // 128) * 8 + ((np.arange(256) % 128) // 32) * 2 + (np.arange(256) % 32) // 16
+    expect = (d32 * np.array(scales, np.float32)[sidx]) * np.asarray(q6, np.float32)
+    assert same_bits(oracle.dequant(Q6_K, blk, 0, 256), expect.astype(np.float32))
+    assert same_bits(npref.dequant(Q6_K, blk), expect.astype(np.float32))
+
+
 # ----------------------------------------------------------------- dots ---
 
 def _offsets(t):
-    bs = {Q8_0: 32, Q4_0: 32, Q4_K: 256}.get(t, 1)
+    bs = {Q8_0: 32, Q4_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}.get(t, 1)
     # aligned rows, unaligned heads and tails, shorter than one block, odd sizes
     return [(0, 2048), (bs, 1024), (7, 900), (max(bs - 3, 1), 5), (3, bs + 9), (0, 17), (64, 1408)]
 
