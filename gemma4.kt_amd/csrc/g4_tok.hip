@@ -247,14 +247,16 @@ __global__ __launch_bounds__(512) void k_tok_q4k(TokArgs a) {
   }
 }
 
-// y[m * y_stride + r] = sum over the column splits, in split order, of their partial sums.
-__global__ void k_tok_reduce(const float *part, int splits, int32_t M, int32_t rows, float *y, int64_t y_stride) {
-  const int64_t n = (int64_t)M * rows;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    float s = part[i];
-    for (int k = 1; k < splits; ++k) s += part[(int64_t)k * n + i];
-    y[(i / rows) * y_stride + i % rows] = s;
-  }
+// y[m * y_stride + r] = sum over the column splits, in split order, of their
+// partial sums; workgroup (bx, m) covers rows 256 bx .. +256 of token m.
+__global__ __launch_bounds__(256) void k_tok_reduce(const float *part, int splits, int32_t M, int32_t rows, float *y,
+                                                    int64_t y_stride) {
+  const int r = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+  if (r >= rows) return;
+  const int64_t n = (int64_t)M * rows, i = (int64_t)m * rows + r;
+  float s = part[i];
+  for (int k = 1; k < splits; ++k) s += part[(int64_t)k * n + i];
+  y[(int64_t)m * y_stride + r] = s;
 }
 
 struct TokShape {
@@ -304,11 +306,8 @@ hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_
   if (sh.splits == 1) return hipGetLastError();
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t n = (int64_t)a.M * a.rows;
-  int blocks = (int)((n + 255) / 256);
-  if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(k_tok_reduce, dim3(blocks), dim3(256), 0, s, (const float *)a.part, sh.splits, a.M, a.rows,
-                     a.y, a.y_stride);
+  hipLaunchKernelGGL(k_tok_reduce, dim3((unsigned)((a.rows + 255) / 256), (unsigned)a.M), dim3(256), 0, s,
+                     (const float *)a.part, sh.splits, a.M, a.rows, a.y, a.y_stride);
   return hipGetLastError();
 }
 
