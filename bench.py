@@ -16,8 +16,9 @@ oracle's restatement of the reference's 512-bit Vector API path on the host
 cores over a bounded sample of the same workload.
 
 Other workloads: --workload q8_0_matvec | q4_0_ffn | q8_0_lm_head |
-q4_k_batched[:M] | moe[:T] | q5_k_matvec | q6_k_matvec; --all prints one line
-per workload.
+q4_k_batched[:M] | moe[:T] | q5_k_matvec | q6_k_matvec | q4_0_ffn_block (the
+FFN with its norms and residual add) | q8_0_lm_head_cap (final norm, soft-cap,
+arg-max); --all prints one line per workload.
 """
 from __future__ import annotations
 
@@ -338,6 +339,94 @@ class MatvecKQuant(Workload):
                 "algorithmic_bytes_per_step": self.step_bytes, "weight_copies": self.copies}
 
 
+class FfnBlockQ4_0(Workload):
+    """The Q4_0 FFN as a whole dense decode block (Llama.kt:355-363): pre-norm
+    fused into the gate/up launch, down, then post-norm plus residual add, with
+    the residual stream x updated in place in device memory."""
+    name = "q4_0_ffn_block_decode_token"
+    dominant_name = ("launch group of g4_ffn_block: k_rows<FmtQ4_0, 32, EPI_GELU_PAIR, NORM> + "
+                     "k_rows<FmtQ4_0, 64, EPI_STORE> + k_rmsnorm (residual)")
+
+    def __init__(self, g4, ctx, torch):
+        import synth
+        c = synth.q4_0_ffn_block()
+        self.c = c
+        dim, hidden = c["dim"], c["hidden"]
+        self.dim, self.hidden, self.eps = dim, hidden, c["eps"]
+        wbytes = c["gate"].nbytes + c["up"].nbytes + c["down"].nbytes
+        self.copies = copies_for(wbytes)
+        F = g4.FloatTensorFactory.create
+        self.w = []
+        for _ in range(self.copies):
+            self.w.append(tuple(F(ctx, Q4_0, c[k], n) for k, n in
+                                (("gate", hidden * dim), ("up", hidden * dim), ("down", dim * hidden))))
+        self.n_pre = F(ctx, 0, c["norm_pre"], dim)
+        self.n_post = F(ctx, 0, c["norm_post"], dim)
+        self.x = torch.from_numpy(c["x"]).cuda()
+        # weights plus activations: gate/up launch reads x and the pre-norm weight and
+        # writes h; down reads h and writes y; the residual launch reads y, the
+        # post-norm weight and x and writes y and x
+        self.step_bytes = wbytes + 4 * (8 * dim + 2 * hidden)
+        self.dominant_bytes = self.step_bytes
+        self.g4, self.ctx = g4, ctx
+
+    def step(self, i):
+        wg, wu, wd = self.w[i % self.copies]
+        self.g4.ffn_block_dev(self.ctx, wg, wu, wd, self.n_pre, self.n_post, self.x, self.dim, self.hidden,
+                              self.eps)
+
+    def cpu_setup(self, oracle):
+        self.oracle = oracle
+
+    def cpu_step(self):
+        c = self.c
+        self.oracle.ffn_block(Q4_0, c["gate"], Q4_0, c["up"], Q4_0, c["down"], c["norm_pre"], c["norm_post"],
+                              c["x"], self.dim, self.hidden, self.eps)
+
+    def config(self):
+        return {"workload": self.name, "format": "Q4_0", "gate_up": [self.hidden, self.dim],
+                "down": [self.dim, self.hidden], "norms": "F32 pre/post", "eps": self.eps,
+                "algorithmic_bytes_per_step": self.step_bytes, "weight_copies": self.copies}
+
+
+class LmHeadCapQ8_0(LmHeadQ8_0):
+    """The Q8_0 LM head behind its final norm and logit soft-cap (Llama.kt:401-407)
+    plus the greedy pick: norm fused into the matvec, cap and arg-max in its epilogue."""
+    name = "q8_0_lm_head_262144x2048_norm_softcap_argmax"
+    dominant_name = "k_rows<FmtQ8_0, 32, EPI_ARGMAX, NORM> (softcap) + k_argmax_final"
+
+    def __init__(self, g4, ctx, torch):
+        import synth
+        c = synth.q8_0_lm_head_block()
+        self.c = c
+        V, D = c["dim0"], c["dim1"]
+        self.V, self.D, self.eps, self.cap = V, D, c["eps"], c["cap"]
+        self.copies = copies_for(c["w"].nbytes)
+        self.w = [g4.FloatTensorFactory.create(ctx, Q8_0, c["w"], V * D) for _ in range(self.copies)]
+        self.norm = g4.FloatTensorFactory.create(ctx, 0, c["norm"], D)
+        self.x = torch.from_numpy(c["x"]).cuda()
+        self.logits = torch.empty(V, dtype=torch.float32, device="cuda")
+        self.idx = torch.zeros(1, dtype=torch.int32, device="cuda")
+        self.step_bytes = c["w"].nbytes + 4 * D + 4 * D + 4 * V + 4
+        self.dominant_bytes = self.step_bytes
+        self.g4, self.ctx = g4, ctx
+
+    def step(self, i):
+        self.g4.lm_head_dev(self.ctx, self.w[i % self.copies], self.norm, self.x, self.logits,
+                            self.idx.data_ptr(), self.V, self.D, self.eps, self.cap)
+
+    def cpu_step(self):
+        self.cpu_step_rows(self.V)
+
+    def cpu_step_rows(self, rows):
+        c = self.c
+        self.oracle.lm_head(Q8_0, c["w"], c["norm"], c["x"], rows, self.D, self.eps, self.cap)
+
+    def config(self):
+        return {"workload": self.name, "format": "Q8_0", "w": [self.V, self.D], "norm": "F32", "eps": self.eps,
+                "softcap": self.cap, "algorithmic_bytes_per_step": self.step_bytes, "weight_copies": self.copies}
+
+
 class CopyCalibration(Workload):
     """A plain fp32 copy of known size (y = x * 1 through torch's elementwise kernel).
 
@@ -371,6 +460,10 @@ def make_workload(spec: str, g4, ctx, torch) -> Workload:
         return MatvecQ8_0(g4, ctx, torch)
     if name == "q8_0_lm_head":
         return LmHeadQ8_0(g4, ctx, torch)
+    if name == "q4_0_ffn_block":
+        return FfnBlockQ4_0(g4, ctx, torch)
+    if name == "q8_0_lm_head_cap":
+        return LmHeadCapQ8_0(g4, ctx, torch)
     if name == "q4_k_batched":
         return BatchedQ4_K(g4, ctx, torch, int(arg or 8))
     if name == "moe":
@@ -530,7 +623,8 @@ def main():
     specs = args.workload.split(",")
     if args.all:
         specs = ["q4_0_ffn", "q8_0_matvec", "q8_0_lm_head", "q4_k_batched:1", "q4_k_batched:8",
-                 "q4_k_batched:32", "q4_k_batched:64", "moe:1", "moe:16", "q5_k_matvec", "q6_k_matvec"]
+                 "q4_k_batched:32", "q4_k_batched:64", "moe:1", "moe:16", "q5_k_matvec", "q6_k_matvec",
+                 "q4_0_ffn_block", "q8_0_lm_head_cap"]
     for s in specs:
         line = run(s, args.steps, args.warmup, args.cpu_seconds, not args.eager)
         print(json.dumps(line), flush=True)

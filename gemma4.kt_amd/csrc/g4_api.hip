@@ -355,6 +355,103 @@ size_t moe_scratch(int32_t T, int32_t dim, int32_t ff, int32_t k, Carve &c, size
   return c.off;
 }
 
+// --- decode step ---
+
+// Norm weights are F32 tensors of at least `size` elements (ModelLoader.kt:281-286
+// reads them as FloatBuffers and rejects any other type).
+int check_norm(const g4_ctx *ctx, const g4_weight *w, int32_t size, const char *name) {
+  G4_TRY(check_weight(ctx, w, name));
+  if (w->type != G4_TYPE_F32) return fail(G4_ERR_UNSUPPORTED, "%s: Conversion to type %d (norm weights are F32)", name, w->type);
+  if (w->n_elems < size)
+    return fail(G4_ERR_OUT_OF_RANGE, "%s holds %lld elements, the norm needs %d", name, (long long)w->n_elems, size);
+  return G4_OK;
+}
+
+int check_eps_cap(float eps, float cap) {
+  if (!(eps >= 0.f) || eps == __builtin_inff()) return fail(G4_ERR_INVALID_ARGUMENT, "rms norm eps must be finite and >= 0");
+  if (cap != cap) return fail(G4_ERR_INVALID_ARGUMENT, "softcap is NaN");
+  return G4_OK;
+}
+
+bool ranges_overlap(const void *a, size_t an, const void *b, size_t bn) {
+  const char *pa = (const char *)a, *pb = (const char *)b;
+  return pa < pb + bn && pb < pa + an;
+}
+
+// out = W . rmsnorm(x): the norm fused into the matvec's x staging when the
+// launch takes it, else a standalone norm into `xn` (dim1 floats) first.  Both
+// give identical bits (the same scale computation, the same element formula).
+int matmul_norm_dev(g4_ctx *ctx, const g4_weight *w, int64_t off, const g4_weight *norm, const float *d_x, float eps,
+                    float *d_xnorm, float *d_out, int32_t dim0, int32_t dim1, int epi, const g4_weight *w_pair,
+                    float *xn, float *d_gu, int32_t *d_index, float softcap) {
+  g4::RowsArgs a = plain_rows(w, off, d_x, d_out, dim0, dim1);
+  if (w_pair) a.W1 = w_pair->d;
+  a.am_val = ctx->am_val;
+  a.am_idx = ctx->am_idx;
+  a.am_out = d_index;
+  a.softcap = softcap;
+  a.norm_w = (const float *)norm->d;
+  a.norm_eps = eps;
+  a.norm_out = d_xnorm;
+  if (!g4::rows_norm_ok(w->type, a, epi == g4::EPI_GELU_PAIR)) {
+    float *dst = d_xnorm ? d_xnorm : xn;
+    G4_TRY(launch_status(g4::launch_rmsnorm(d_x, (const float *)norm->d, dst, nullptr, 1, dim1, eps,
+                                            G4_NORM_WEIGHT_AFTER, ctx->stream), "rmsnorm"));
+    a.x = dst;
+    a.norm_w = nullptr;
+    a.norm_out = nullptr;
+  }
+  return launch_status(g4::launch_rows(w->type, epi, a, 1, ctx->dev, d_gu, ctx->stream), "matmul_norm");
+}
+
+// Scratch floats matmul_norm_dev may need for the standalone norm.
+int64_t norm_scratch_floats(const g4_weight *w, int64_t off, int32_t dim0, int32_t dim1, bool paired) {
+  g4::RowsArgs a = plain_rows(w, off, nullptr, nullptr, dim0, dim1);
+  a.norm_w = (const float *)1;
+  return g4::rows_norm_ok(w->type, a, paired) ? 0 : dim1;
+}
+
+// Llama.kt:355-363 (dense FFN block), in place on d_x.
+int ffn_block_dev(g4_ctx *ctx, const g4_weight *wg, const g4_weight *wu, const g4_weight *wd, const g4_weight *n_pre,
+                  const g4_weight *n_post, float *d_x, int32_t dim, int32_t hidden, float eps, float *d_h, float *d_y,
+                  float *d_gu, float *xn) {
+  // xb = rmsnorm(x, rmsFfnWeight); h = gelu(w1 xb) * (w3 xb)
+  G4_TRY(matmul_norm_dev(ctx, wg, 0, n_pre, d_x, eps, nullptr, d_h, hidden, dim, g4::EPI_GELU_PAIR, wu, xn, d_gu,
+                         nullptr, 0.f));
+  // xb = w2 h
+  g4::RowsArgs b = plain_rows(wd, 0, d_h, d_y, dim, hidden);
+  G4_TRY(launch_status(g4::launch_rows(wd->type, g4::EPI_STORE, b, 1, ctx->dev, nullptr, ctx->stream), "ffn_block"));
+  // xb = rmsnorm(xb, postFfwNorm); x += xb
+  return launch_status(g4::launch_rmsnorm(d_y, (const float *)n_post->d, d_y, d_x, 1, dim, eps, G4_NORM_WEIGHT_AFTER,
+                                          ctx->stream), "ffn_block");
+}
+
+void ffn_block_scratch(const g4_weight *wg, int32_t dim, int32_t hidden, Carve &c, size_t *h, size_t *y, size_t *gu,
+                       size_t *xn) {
+  *h = c.add(sizeof(float) * (size_t)hidden);
+  *y = c.add(sizeof(float) * (size_t)dim);
+  *gu = c.add(sizeof(float) * 2 * (size_t)hidden);
+  *xn = c.add(sizeof(float) * (size_t)norm_scratch_floats(wg, 0, hidden, dim, true));
+}
+
+int check_ffn_block(g4_ctx *ctx, const g4_weight *wg, const g4_weight *wu, const g4_weight *wd, const g4_weight *n_pre,
+                    const g4_weight *n_post, int32_t dim, int32_t hidden, float eps) {
+  G4_TRY(check_ffn(ctx, wg, wu, wd, dim, hidden));
+  G4_TRY(check_norm(ctx, n_pre, dim, "norm_pre"));
+  G4_TRY(check_norm(ctx, n_post, dim, "norm_post"));
+  return check_eps_cap(eps, 0.f);
+}
+
+int check_lm_head(g4_ctx *ctx, const g4_weight *w, const g4_weight *norm, int32_t vocab, int32_t dim, float eps,
+                  float cap) {
+  G4_TRY(check_weight(ctx, w, "w_cls"));
+  if (vocab <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "argmax needs vocab > 0 (FloatTensor.kt:54)");
+  if (dim <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "dim must be positive (%d)", dim);
+  G4_TRY(check_rows(w, 0, vocab, dim));
+  G4_TRY(check_norm(ctx, norm, dim, "norm_final"));
+  return check_eps_cap(eps, cap);
+}
+
 }  // namespace
 
 // =============================================================== C ABI ====
@@ -881,6 +978,162 @@ int g4_moe_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down,
   char *s = ctx->scratch;
   return moe_dev(ctx, w_gate_up, w_down, ne, d_X, T, dim, ff, d_ids, d_weights, k, d_Y, (float *)(s + oh),
                  (float *)(s + oys), (float *)(s + ogu));
+}
+
+// ---------------------------------------------------------- decode step ----
+
+int g4_rmsnorm_dev(g4_ctx *ctx, const g4_weight *weight, const float *d_x, float *d_out, int32_t n_vec, int32_t size,
+                   float eps, int form) {
+  G4_TRY(check_ctx(ctx));
+  if (form != G4_NORM_WEIGHT_AFTER && form != G4_NORM_WEIGHT_FIRST && form != G4_NORM_NO_WEIGHT)
+    return fail(G4_ERR_INVALID_ARGUMENT, "unknown norm form %d", form);
+  if (n_vec < 0 || size < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative n_vec or size (%d, %d)", n_vec, size);
+  G4_TRY(check_eps_cap(eps, 0.f));
+  if (form != G4_NORM_NO_WEIGHT) G4_TRY(check_norm(ctx, weight, size, "weight"));
+  if (n_vec == 0 || size == 0) return ok();
+  if (!d_x || !d_out) return fail(G4_ERR_INVALID_ARGUMENT, "x/out is null");
+  const size_t bytes = sizeof(float) * (size_t)n_vec * size;
+  if (d_x != d_out && ranges_overlap(d_x, bytes, d_out, bytes))
+    return fail(G4_ERR_INVALID_ARGUMENT, "out overlaps x without being x");
+  G4_TRY(use_device(ctx));
+  const float *w = form == G4_NORM_NO_WEIGHT ? nullptr : (const float *)weight->d;
+  return launch_status(g4::launch_rmsnorm(d_x, w, d_out, nullptr, n_vec, size, eps, form, ctx->stream), "rmsnorm");
+}
+
+int g4_rmsnorm_add_dev(g4_ctx *ctx, const g4_weight *weight, float *d_v, float *d_x, int32_t size, float eps) {
+  G4_TRY(check_ctx(ctx));
+  if (size < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative size %d", size);
+  G4_TRY(check_eps_cap(eps, 0.f));
+  G4_TRY(check_norm(ctx, weight, size, "weight"));
+  if (size == 0) return ok();
+  if (!d_v || !d_x) return fail(G4_ERR_INVALID_ARGUMENT, "v/x is null");
+  const size_t bytes = sizeof(float) * (size_t)size;
+  if (ranges_overlap(d_v, bytes, d_x, bytes)) return fail(G4_ERR_INVALID_ARGUMENT, "v overlaps x");
+  G4_TRY(use_device(ctx));
+  return launch_status(g4::launch_rmsnorm(d_v, (const float *)weight->d, d_v, d_x, 1, size, eps,
+                                          G4_NORM_WEIGHT_AFTER, ctx->stream), "rmsnorm_add");
+}
+
+int g4_add_dev(g4_ctx *ctx, float *d_x, const float *d_that, int32_t n) {
+  G4_TRY(check_ctx(ctx));
+  if (n < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative size %d", n);
+  if (n == 0) return ok();
+  if (!d_x || !d_that) return fail(G4_ERR_INVALID_ARGUMENT, "x/that is null");
+  G4_TRY(use_device(ctx));
+  return launch_status(g4::launch_add(d_x, d_that, n, ctx->stream), "add");
+}
+
+int g4_softcap_dev(g4_ctx *ctx, float *d_v, int32_t n, float cap) {
+  G4_TRY(check_ctx(ctx));
+  if (n < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative size %d", n);
+  if (!(cap > 0.f) || cap == __builtin_inff()) return fail(G4_ERR_INVALID_ARGUMENT, "softcap must be finite and > 0");
+  if (n == 0) return ok();
+  if (!d_v) return fail(G4_ERR_INVALID_ARGUMENT, "v is null");
+  G4_TRY(use_device(ctx));
+  return launch_status(g4::launch_softcap(d_v, n, cap, ctx->stream), "softcap");
+}
+
+int g4_matmul_norm_dev(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const g4_weight *norm, const float *d_x,
+                       float eps, float *d_xnorm, float *d_out, int32_t dim0, int32_t dim1) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_weight(ctx, w, "weight"));
+  G4_TRY(check_rows(w, this_offset, dim0, dim1));
+  G4_TRY(check_norm(ctx, norm, dim1, "norm"));
+  G4_TRY(check_eps_cap(eps, 0.f));
+  if ((!d_x && dim1 > 0) || (!d_out && dim0 > 0)) return fail(G4_ERR_INVALID_ARGUMENT, "x/out is null");
+  if (d_xnorm && dim1 > 0 && ranges_overlap(d_xnorm, sizeof(float) * (size_t)dim1, d_x, sizeof(float) * (size_t)dim1))
+    return fail(G4_ERR_INVALID_ARGUMENT, "xnorm overlaps x");
+  G4_TRY(use_device(ctx));
+  if (dim1 == 0) {
+    if (dim0 > 0) G4_HIP(hipMemsetAsync(d_out, 0, sizeof(float) * (size_t)dim0, ctx->stream), "hipMemsetAsync");
+    return ok();
+  }
+  if (dim0 == 0) {
+    if (!d_xnorm) return ok();
+    return launch_status(g4::launch_rmsnorm(d_x, (const float *)norm->d, d_xnorm, nullptr, 1, dim1, eps,
+                                            G4_NORM_WEIGHT_AFTER, ctx->stream), "rmsnorm");
+  }
+  // launches that cannot take the fused norm (rows not 64-aligned, several
+  // column passes) normalise into scratch first
+  float *xn = nullptr;
+  if (!d_xnorm && norm_scratch_floats(w, this_offset, dim0, dim1, false) > 0) {
+    Carve c;
+    size_t o = c.add(sizeof(float) * (size_t)dim1);
+    G4_TRY(ensure_scratch(ctx, c.off));
+    xn = (float *)(ctx->scratch + o);
+  }
+  return matmul_norm_dev(ctx, w, this_offset, norm, d_x, eps, d_xnorm, d_out, dim0, dim1, g4::EPI_STORE, nullptr, xn,
+                         nullptr, nullptr, 0.f);
+}
+
+int g4_ffn_block(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const g4_weight *w_down,
+                 const g4_weight *norm_pre, const g4_weight *norm_post, float *x, int32_t dim, int32_t hidden,
+                 float eps) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_ffn_block(ctx, w_gate, w_up, w_down, norm_pre, norm_post, dim, hidden, eps));
+  if (!x) return fail(G4_ERR_INVALID_ARGUMENT, "x is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t ox = c.add(sizeof(float) * (size_t)dim), oh, oy, og, on;
+  ffn_block_scratch(w_gate, dim, hidden, c, &oh, &oy, &og, &on);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  char *s = ctx->scratch;
+  G4_TRY(copy_in(ctx, s + ox, x, sizeof(float) * (size_t)dim));
+  G4_TRY(ffn_block_dev(ctx, w_gate, w_up, w_down, norm_pre, norm_post, (float *)(s + ox), dim, hidden, eps,
+                       (float *)(s + oh), (float *)(s + oy), (float *)(s + og), (float *)(s + on)));
+  G4_TRY(copy_out(ctx, x, s + ox, sizeof(float) * (size_t)dim));
+  return finish(ctx);
+}
+
+int g4_ffn_block_dev(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const g4_weight *w_down,
+                     const g4_weight *norm_pre, const g4_weight *norm_post, float *d_x, int32_t dim, int32_t hidden,
+                     float eps) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_ffn_block(ctx, w_gate, w_up, w_down, norm_pre, norm_post, dim, hidden, eps));
+  if (!d_x) return fail(G4_ERR_INVALID_ARGUMENT, "x is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t oh, oy, og, on;
+  ffn_block_scratch(w_gate, dim, hidden, c, &oh, &oy, &og, &on);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  char *s = ctx->scratch;
+  return ffn_block_dev(ctx, w_gate, w_up, w_down, norm_pre, norm_post, d_x, dim, hidden, eps, (float *)(s + oh),
+                       (float *)(s + oy), (float *)(s + og), (float *)(s + on));
+}
+
+int g4_lm_head(g4_ctx *ctx, const g4_weight *w_cls, const g4_weight *norm_final, const float *x, float *logits,
+               int32_t *index, int32_t vocab, int32_t dim, float eps, float softcap) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_lm_head(ctx, w_cls, norm_final, vocab, dim, eps, softcap));
+  if (!x || !index) return fail(G4_ERR_INVALID_ARGUMENT, "x/index is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t ox = c.add(sizeof(float) * (size_t)dim), on = c.add(sizeof(float) * (size_t)dim),
+         oy = c.add(sizeof(float) * (size_t)vocab), oi = c.add(sizeof(int32_t));
+  G4_TRY(ensure_scratch(ctx, c.off));
+  char *s = ctx->scratch;
+  G4_TRY(copy_in(ctx, s + ox, x, sizeof(float) * (size_t)dim));
+  G4_TRY(matmul_norm_dev(ctx, w_cls, 0, norm_final, (const float *)(s + ox), eps, nullptr, (float *)(s + oy), vocab,
+                         dim, g4::EPI_ARGMAX, nullptr, (float *)(s + on), nullptr, (int32_t *)(s + oi), softcap));
+  if (logits) G4_TRY(copy_out(ctx, logits, s + oy, sizeof(float) * (size_t)vocab));
+  G4_TRY(copy_out(ctx, index, s + oi, sizeof(int32_t)));
+  return finish(ctx);
+}
+
+int g4_lm_head_dev(g4_ctx *ctx, const g4_weight *w_cls, const g4_weight *norm_final, const float *d_x, float *d_xnorm,
+                   float *d_logits, int32_t *d_index, int32_t vocab, int32_t dim, float eps, float softcap) {
+  G4_TRY(check_ctx(ctx));
+  G4_TRY(check_lm_head(ctx, w_cls, norm_final, vocab, dim, eps, softcap));
+  if (!d_x || !d_index) return fail(G4_ERR_INVALID_ARGUMENT, "x/index is null");
+  if (d_xnorm && ranges_overlap(d_xnorm, sizeof(float) * (size_t)dim, d_x, sizeof(float) * (size_t)dim))
+    return fail(G4_ERR_INVALID_ARGUMENT, "xnorm overlaps x");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t oy = c.add(d_logits ? 0 : sizeof(float) * (size_t)vocab), on = c.add(sizeof(float) * (size_t)dim);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  float *dy = d_logits ? d_logits : (float *)(ctx->scratch + oy);
+  return matmul_norm_dev(ctx, w_cls, 0, norm_final, d_x, eps, d_xnorm, dy, vocab, dim, g4::EPI_ARGMAX, nullptr,
+                         (float *)(ctx->scratch + on), nullptr, d_index, softcap);
 }
 
 }  // extern "C"

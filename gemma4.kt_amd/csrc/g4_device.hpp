@@ -586,4 +586,45 @@ G4_DEV float gelu_ref(float xf) {
   return (float)(0.5 * x * (1.0 + tanh(inner)));
 }
 
+// ------------------------------------------------------------ rms norm ----
+// The three ways Llama.kt applies the rms scale s to element x with weight w:
+// rmsnorm(out, x, weight, size, eps) (Llama.kt:27-37) computes w * (s * x); the
+// offset overload (Llama.kt:39-59) computes w * s * x left to right; and
+// rmsnormNoWeight (Llama.kt:61-78) computes s * x.
+enum : int { NORM_WEIGHT_AFTER = 0, NORM_WEIGHT_FIRST = 1, NORM_NO_WEIGHT = 2 };
+
+G4_DEV float norm_apply(int form, float w, float s, float x) {
+  if (form == NORM_WEIGHT_AFTER) return __fmul_rn(w, __fmul_rn(s, x));
+  if (form == NORM_WEIGHT_FIRST) return __fmul_rn(__fmul_rn(w, s), x);
+  return __fmul_rn(s, x);
+}
+
+// ss = fp32 sum of squares -> s = (float)(1.0 / sqrt((double)(ss / size + eps))),
+// each step rounded as in the reference (fp32 divide and add, double sqrt and divide).
+G4_DEV float rms_scale(float ss, int32_t size, float eps) {
+  const float m = __fadd_rn(__fdiv_rn(ss, (float)size), eps);
+  return (float)__ddiv_rn(1.0, __dsqrt_rn((double)m));
+}
+
+G4_DEV float sq_acc(float acc, float v) { return __builtin_fmaf(v, v, acc); }
+
+// Sum over a 256-thread workgroup, the same value in every thread: the wave
+// butterfly (both partners of a pair add the same two values, so every lane
+// ends with identical bits), then the four wave sums in wave order.  `red` is
+// four floats of LDS; call once per kernel.  The standalone rms norm and the
+// matvec kernels' fused input norm both feed it the same per-thread partials
+// (thread t sums 16-byte segments t, t + 256, ... holding elements 4s..4s+3, in
+// element order), so fused and standalone norms give identical scales.
+G4_DEV float block_sum256(float v, float *red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return __fadd_rn(__fadd_rn(__fadd_rn(red[0], red[1]), red[2]), red[3]);
+}
+
+// Llama.kt:403-406 final logit soft-capping: cap * (float)tanh((double)(v / cap)).
+G4_DEV float softcap_ref(float v, float cap) {
+  return __fmul_rn(cap, (float)tanh((double)__fdiv_rn(v, cap)));
+}
+
 }  // namespace g4

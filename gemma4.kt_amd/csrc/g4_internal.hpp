@@ -33,6 +33,16 @@ struct RowsArgs {
   float *am_val;
   int32_t *am_idx;
   int32_t *am_out;
+  // EPI_ARGMAX: logits are soft-capped (Llama.kt:403-406) before the store and the
+  // arg-max when softcap > 0
+  float softcap;
+  // Input rms norm (Llama.kt:27-37) fused into the x staging when norm_w != null:
+  // every workgroup computes the scale of x and stages norm_w[j] * (s * x[j]); the
+  // first workgroup also stores the normalised x to norm_out (when not null, and
+  // not aliasing x).  Single-segment, single-pass launches only (rows_norm_ok).
+  const float *norm_w;
+  float norm_eps;
+  float *norm_out;
 };
 
 // Device facts used for launch sizing.
@@ -42,6 +52,8 @@ struct DevInfo {
 
 // True when rows of (type, offsets, dim1) take the 64-element chunk kernels.
 bool rows_fast_ok(int type, const RowsArgs &a, bool paired);
+// True when such a launch can also take the fused input norm (one column pass).
+bool rows_norm_ok(int type, const RowsArgs &a, bool paired);
 
 // Launch the matvec engine over `segments` segments.  For EPI_GELU_PAIR the
 // launch writes h[r] = gelu(W0 row r . x) * (W1 row r . x); on the generic path
@@ -81,5 +93,13 @@ hipError_t launch_route(const float *logits, int32_t T, int32_t n_experts, int32
                         const float *expert_scale, int32_t *ids, float *weights, hipStream_t stream);
 hipError_t launch_moe_combine(const float *ys, const float *weights, int32_t T, int32_t k, int32_t dim, float *Y,
                               hipStream_t stream);
+
+// Decode-step element-wise work.  rms norm of n_vec vectors of `size` floats
+// (vector v at x + v * size; w shared, null for NORM_NO_WEIGHT); out may alias
+// x; when resid != null also resid += out.
+hipError_t launch_rmsnorm(const float *x, const float *w, float *out, float *resid, int32_t n_vec, int32_t size,
+                          float eps, int form, hipStream_t stream);
+hipError_t launch_add(float *x, const float *that, int64_t n, hipStream_t stream);
+hipError_t launch_softcap(float *v, int64_t n, float cap, hipStream_t stream);
 
 }  // namespace g4

@@ -14,10 +14,15 @@
 #include <float.h>
 #include <limits.h>
 
+#include "../../include/g4hip.h"
 #include "g4_device.hpp"
 #include "g4_internal.hpp"
 
 namespace g4 {
+
+static_assert(NORM_WEIGHT_AFTER == G4_NORM_WEIGHT_AFTER && NORM_WEIGHT_FIRST == G4_NORM_WEIGHT_FIRST &&
+                  NORM_NO_WEIGHT == G4_NORM_NO_WEIGHT,
+              "norm forms of the C ABI");
 
 // ------------------------------------------------------------ arg-max ----
 // Cross-block (value, index) reduction in two launches.  Inside one launch a
@@ -58,7 +63,7 @@ __global__ __launch_bounds__(256) void k_argmax_final(const float *pv, const int
 
 // --------------------------------------------------------------- engine ----
 
-template <class F, int LPR, int CPL, int EPI, bool MULTI>
+template <class F, int LPR, int CPL, int EPI, bool MULTI, bool NORM>
 __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1;  // row steps per tile (about F::RT chunk loads per lane)
   constexpr int RPW = 64 / LPR;                  // rows in flight per step (one per lane group)
@@ -70,7 +75,9 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   static_assert(RT >= 1, "tile");
   static_assert(EPI != EPI_GELU_PAIR || (RT >= 2 && CPL == 1), "paired tiles: gate and up steps, one pass");
   static_assert(XSEG >= 1 && XSEG * 256 == NCH * 16, "x staging");
+  static_assert(!(NORM && MULTI), "the fused norm needs all of x in one pass");
   __shared__ u32x4 xl[NCH * 16];
+  __shared__ float red[4];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: tile loop control stays scalar
@@ -147,6 +154,27 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     gq_n = 0;
   };
 
+  // EPI_ARGMAX (one column pass): the same kind of queue for the logits, so the
+  // soft-cap's double tanh, the store and the arg-max update run once per 64
+  // rows with every lane busy (coalesced stores), not once per tile.
+  constexpr bool AQ = EPI == EPI_ARGMAX && !MULTI;
+  __shared__ float aq[AQ ? 4 : 1][64];
+  int aq_n = 0, aq_row = t0 * LRT;
+  auto aq_flush = [&]() {
+    if (lane < aq_n) {
+      const int lr = aq_row + lane;
+      float val = aq[AQ ? wid : 0][lane];
+      if (a.softcap > 0.f) val = softcap_ref(val, a.softcap);
+      if (lr < a.rows) {
+        if (y) y[lr] = val;
+        const float key = am_key(val, lr);
+        if (am_better(key, lr, best_v, best_i)) best_v = key, best_i = lr;
+      }
+    }
+    aq_row += aq_n;
+    aq_n = 0;
+  };
+
   auto finish_tile = [&](int t, int pass, const uint32_t (&D)[RT][CPL][NDW], const bool (&ok)[RT][CPL],
                          const int64_t (&E)[RT][CPL], const float (&xv)[CPL][64], const float (&xs)[CPL][F::NS > 0 ? F::NS : 1]) {
     float v[RT];
@@ -168,24 +196,27 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
       if (writer && k < RT / 2) gq[wid][gq_n + (k % (RT / 2)) * RPW + gi] = make_float2(r, up);
       gq_n += LRT;
       if (gq_n + LRT > 64) gq_flush();
+    } else if constexpr (AQ) {
+      if (writer) aq[wid][aq_n + k * RPW + gi] = r;
+      aq_n += LRT;
+      if (aq_n + LRT > 64) aq_flush();
     } else {
       const int lr = t * LRT + k * RPW + gi;
       if (writer && lr < a.rows) {
         float val = r;
-        if (y) {
-          // only the multi-pass kernels read back (a load here would make every
-          // single-pass tile wait for the prefetched one: vmcnt retires in order)
-          if constexpr (MULTI) {
-            if (pass > 0) val += y[lr];
-          }
-          y[lr] = val;
+        // only the multi-pass kernels read back (a load here would make every
+        // single-pass tile wait for the prefetched one: vmcnt retires in order)
+        if constexpr (MULTI) {
+          if (y && pass > 0) val += y[lr];
         }
         if constexpr (EPI == EPI_ARGMAX) {
           if (!MULTI || pass == passes - 1) {
+            if (a.softcap > 0.f) val = softcap_ref(val, a.softcap);
             const float key = am_key(val, lr);
             if (am_better(key, lr, best_v, best_i)) best_v = key, best_i = lr;
           }
         }
+        if (y) y[lr] = val;
       }
     }
   };
@@ -199,14 +230,43 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     // does the thread wait for x (vmcnt retires in issue order, so that wait
     // never covers the weight latency; the barrier waits on LDS only).
     u32x4a4 xr[XSEG];
+    u32x4a4 wr[NORM ? XSEG : 1];
 #pragma unroll
     for (int j = 0; j < XSEG; ++j) {
       const int s = j * 256 + tid, c = pass * NCH + (s >> 4);
       // dword alignment is all a caller's x guarantees; gfx950 takes 128-bit loads at that alignment
       xr[j] = ((const u32x4a4 *)(x + (int64_t)(c < C ? c : 0) * 64))[s & 15];
+      if constexpr (NORM) wr[j] = ((const u32x4a4 *)(a.norm_w + (int64_t)(c < C ? c : 0) * 64))[s & 15];
     }
     load_tile(t0, pass, t0 < t1, DA, okA, EA);
     if (MULTI && pass > 0) __syncthreads();  // every wave has read the previous pass's x
+    if constexpr (NORM) {
+      // Llama.kt:27-37 on the staged x: thread tid holds 16-byte segments
+      // tid + 256 j (elements 4s..4s+3), the element map of k_rmsnorm, so the
+      // scale is bit-identical to the standalone norm's
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < XSEG; ++j) {
+        const int s = j * 256 + tid, c = s >> 4;
+        const uint32_t m = opaque(c < C ? ~0u : 0u);
+        xr[j] = u32x4a4{xr[j].x & m, xr[j].y & m, xr[j].z & m, xr[j].w & m};
+        acc = sq_acc(acc, __uint_as_float(xr[j].x));
+        acc = sq_acc(acc, __uint_as_float(xr[j].y));
+        acc = sq_acc(acc, __uint_as_float(xr[j].z));
+        acc = sq_acc(acc, __uint_as_float(xr[j].w));
+      }
+      const float sc = rms_scale(block_sum256(acc, red), a.dim1, a.norm_eps);
+      const bool keep = a.norm_out && blockIdx.x == 0 && blockIdx.y == 0;
+#pragma unroll
+      for (int j = 0; j < XSEG; ++j) {
+        const int s = j * 256 + tid, c = s >> 4;
+        xr[j].x = __float_as_uint(norm_apply(NORM_WEIGHT_AFTER, __uint_as_float(wr[j].x), sc, __uint_as_float(xr[j].x)));
+        xr[j].y = __float_as_uint(norm_apply(NORM_WEIGHT_AFTER, __uint_as_float(wr[j].y), sc, __uint_as_float(xr[j].y)));
+        xr[j].z = __float_as_uint(norm_apply(NORM_WEIGHT_AFTER, __uint_as_float(wr[j].z), sc, __uint_as_float(xr[j].z)));
+        xr[j].w = __float_as_uint(norm_apply(NORM_WEIGHT_AFTER, __uint_as_float(wr[j].w), sc, __uint_as_float(xr[j].w)));
+        if (keep && c < C) ((u32x4a4 *)(a.norm_out + (int64_t)c * 64))[s & 15] = xr[j];
+      }
+    }
 #pragma unroll
     for (int j = 0; j < XSEG; ++j) {
       const int s = j * 256 + tid, ch = s >> 4, c = pass * NCH + ch;
@@ -253,6 +313,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   }
 
   if constexpr (EPI == EPI_GELU_PAIR) gq_flush();
+  if constexpr (AQ) aq_flush();
   if constexpr (EPI == EPI_ARGMAX) am_partial(best_v, best_i, a.am_val, a.am_idx);
 }
 
@@ -394,6 +455,100 @@ __global__ void k_moe_combine(const float *ys, const float *w, int32_t T, int32_
   }
 }
 
+// --------------------------------------------------------- decode step ----
+// rms norm of vector blockIdx.x (x + v * size, `size` floats), one workgroup each:
+// rmsnorm / offset rmsnorm / rmsnormNoWeight of Llama.kt:27-78 by `form`.  The
+// sum of squares uses block_sum256's element map; out may alias x (every
+// element is read before the scale's barrier and rewritten by its reader);
+// resid != null: resid += out (addInPlace, MutableFloatTensor.kt:28-37).
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *x, const float *w, float *out, float *resid,
+                                                 int32_t size, float eps, int form) {
+  __shared__ float red[4];
+  const int64_t base = (int64_t)blockIdx.x * size;
+  const float *xv = x + base;
+  float acc = 0.f;
+  for (int64_t s = threadIdx.x; s * 4 < size; s += 256)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int64_t i = 4 * s + c;
+      acc = sq_acc(acc, i < size ? xv[i] : 0.f);
+    }
+  const float sc = rms_scale(block_sum256(acc, red), size, eps);
+  for (int i = threadIdx.x; i < size; i += 256) {
+    const float o = norm_apply(form, form == NORM_NO_WEIGHT ? 1.f : w[i], sc, xv[i]);
+    out[base + i] = o;
+    if (resid) resid[base + i] = __fadd_rn(resid[base + i], o);
+  }
+}
+
+// The same for sizes that are a multiple of 4 up to 1024 * VPT: every load
+// (x, weight, residual; 16-byte segments tid + 256 j) is issued up front and the
+// vector stays in registers, so the kernel makes one round trip to memory.
+// Null weight / residual pointers read x instead (no branch around a load).
+template <int VPT>
+__global__ __launch_bounds__(256) void k_rmsnorm_v(const float *x, const float *w, float *out, float *resid,
+                                                   int32_t size, float eps, int form) {
+  __shared__ float red[4];
+  const int64_t base = (int64_t)blockIdx.x * size;
+  const int tid = threadIdx.x;
+  const float *wp = w ? w : x + base;
+  const float *rp = resid ? resid + base : x + base;
+  u32x4a4 xv[VPT], wv[VPT], rv[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int s = j * 256 + tid;
+    const int64_t e = 4 * s < size ? 4 * s : 0;
+    xv[j] = *(const u32x4a4 *)(x + base + e);
+    wv[j] = *(const u32x4a4 *)(wp + e);
+    rv[j] = *(const u32x4a4 *)(rp + e);
+  }
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const uint32_t m = opaque(4 * (j * 256 + tid) < size ? ~0u : 0u);
+    xv[j] = u32x4a4{xv[j].x & m, xv[j].y & m, xv[j].z & m, xv[j].w & m};
+    acc = sq_acc(acc, __uint_as_float(xv[j].x));
+    acc = sq_acc(acc, __uint_as_float(xv[j].y));
+    acc = sq_acc(acc, __uint_as_float(xv[j].z));
+    acc = sq_acc(acc, __uint_as_float(xv[j].w));
+  }
+  const float sc = rms_scale(block_sum256(acc, red), size, eps);
+  const bool nw = form == NORM_NO_WEIGHT;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int s = j * 256 + tid;
+    if (4 * s >= size) continue;
+    float o[4];
+    const float xs[4] = {__uint_as_float(xv[j].x), __uint_as_float(xv[j].y), __uint_as_float(xv[j].z),
+                         __uint_as_float(xv[j].w)};
+    const float ws[4] = {__uint_as_float(wv[j].x), __uint_as_float(wv[j].y), __uint_as_float(wv[j].z),
+                         __uint_as_float(wv[j].w)};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = norm_apply(form, nw ? 1.f : ws[c], sc, xs[c]);
+    *(u32x4a4 *)(out + base + 4 * s) = u32x4a4{__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
+                                               __float_as_uint(o[3])};
+    if (resid) {
+      const float rs[4] = {__uint_as_float(rv[j].x), __uint_as_float(rv[j].y), __uint_as_float(rv[j].z),
+                           __uint_as_float(rv[j].w)};
+      *(u32x4a4 *)(resid + base + 4 * s) =
+          u32x4a4{__float_as_uint(__fadd_rn(rs[0], o[0])), __float_as_uint(__fadd_rn(rs[1], o[1])),
+                  __float_as_uint(__fadd_rn(rs[2], o[2])), __float_as_uint(__fadd_rn(rs[3], o[3]))};
+    }
+  }
+}
+
+// x[i] = x[i] + that[i] (MutableFloatTensor.kt:28-37).
+__global__ void k_add(float *x, const float *that, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    x[i] = __fadd_rn(x[i], that[i]);
+}
+
+// Llama.kt:403-406 soft-capping in place.
+__global__ void k_softcap(float *v, int64_t n, float cap) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    v[i] = softcap_ref(v[i], cap);
+}
+
 // ---------------------------------------------------------------- launchers ----
 
 bool rows_fast_ok(int type, const RowsArgs &a, bool paired) {
@@ -409,6 +564,12 @@ bool rows_fast_ok(int type, const RowsArgs &a, bool paired) {
   }
 }
 
+bool rows_norm_ok(int type, const RowsArgs &a, bool paired) {
+  if (!rows_fast_ok(type, a, paired)) return false;
+  // one column pass: up to 64 lanes x 2 chunks per row (x 1 for the paired kernel)
+  return (a.dim1 / 64) <= (paired ? 64 : 128);
+}
+
 int max_argmax_blocks(const DevInfo &dev) { return dev.cu_count * 8; }
 
 template <class F, int LPR, int CPL>
@@ -416,25 +577,28 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
   constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1, RPW = 64 / LPR, TR = RT * RPW;
   typedef void (*Kernel)(RowsArgs);
   const bool multi = (a.dim1 / 64) > LPR * CPL;
+  const bool norm = a.norm_w != nullptr;
+  if (norm && (multi || segments != 1)) return hipErrorInvalidValue;
   Kernel k = nullptr;
   if (epi == EPI_STORE) {
-    k = k_rows<F, LPR, CPL, EPI_STORE, false>;
+    k = norm ? k_rows<F, LPR, CPL, EPI_STORE, false, true> : k_rows<F, LPR, CPL, EPI_STORE, false, false>;
     if constexpr (LPR == 64 && CPL == 2)
-      if (multi) k = k_rows<F, LPR, CPL, EPI_STORE, true>;
+      if (multi) k = k_rows<F, LPR, CPL, EPI_STORE, true, false>;
   } else if (epi == EPI_ARGMAX) {
-    k = k_rows<F, LPR, CPL, EPI_ARGMAX, false>;
+    k = norm ? k_rows<F, LPR, CPL, EPI_ARGMAX, false, true> : k_rows<F, LPR, CPL, EPI_ARGMAX, false, false>;
     if constexpr (LPR == 64 && CPL == 2)
-      if (multi) k = k_rows<F, LPR, CPL, EPI_ARGMAX, true>;
+      if (multi) k = k_rows<F, LPR, CPL, EPI_ARGMAX, true, false>;
   } else {
-    if constexpr (CPL == 1 && F::RT >= 2) k = k_rows<F, LPR, 1, EPI_GELU_PAIR, false>;
+    if constexpr (CPL == 1 && F::RT >= 2)
+      k = norm ? k_rows<F, LPR, 1, EPI_GELU_PAIR, false, true> : k_rows<F, LPR, 1, EPI_GELU_PAIR, false, false>;
   }
   if (!k) return hipErrorInvalidValue;
   if (multi && !(LPR == 64 && CPL == 2)) return hipErrorInvalidValue;
 
   // Resident 256-thread workgroups per CU for this kernel (register-limited);
   // the launch fills exactly that many waves when there are tiles enough.
-  static int resident[3][2];
-  int &res = resident[epi][multi ? 1 : 0];
+  static int resident[3][2][2];
+  int &res = resident[epi][multi ? 1 : 0][norm ? 1 : 0];
   if (res == 0) {
     int nb = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 256, 0) != hipSuccess || nb < 1) nb = 2;
@@ -519,6 +683,7 @@ hipError_t launch_rows(int type, int epi, const RowsArgs &a, int segments, const
   }
   // generic path
   if (epi == EPI_GELU_PAIR) {
+    if (a.norm_w) return hipErrorInvalidValue;
     RowsArgs g = a;
     g.y = scratch;
     g.y_stride = 2 * (int64_t)a.rows;
@@ -531,8 +696,13 @@ hipError_t launch_rows(int type, int epi, const RowsArgs &a, int segments, const
                        a.y_stride);
     return hipGetLastError();
   }
+  if (a.norm_w) return hipErrorInvalidValue;  // callers normalise x first when rows_norm_ok fails
   hipError_t e = launch_generic(type, a, 1, segments, dev, s);
   if (e != hipSuccess || epi != EPI_ARGMAX) return e;
+  if (a.softcap > 0.f) {
+    e = launch_softcap(a.y, a.rows, a.softcap, s);
+    if (e != hipSuccess) return e;
+  }
   return launch_argmax(a.y, a.rows, a.am_val, a.am_idx, a.am_out, dev, s);
 }
 
@@ -571,6 +741,40 @@ hipError_t launch_route(const float *logits, int32_t T, int32_t n_experts, int32
                         const float *expert_scale, int32_t *ids, float *weights, hipStream_t s) {
   if (n_experts > ROUTE_MAX_E) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_route, dim3(T), dim3(64), 0, s, logits, n_experts, k, renorm, expert_scale, ids, weights);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const float *x, const float *w, float *out, float *resid, int32_t n_vec, int32_t size,
+                          float eps, int form, hipStream_t s) {
+  if (n_vec <= 0 || size <= 0) return hipSuccess;
+  if (form < NORM_WEIGHT_AFTER || form > NORM_NO_WEIGHT || (form != NORM_NO_WEIGHT && !w)) return hipErrorInvalidValue;
+  if (form == NORM_NO_WEIGHT) w = nullptr;
+  if (size % 4 == 0 && size <= 8192) {
+    const int vpt = (size + 1023) / 1024;
+    if (vpt == 1) hipLaunchKernelGGL(k_rmsnorm_v<1>, dim3(n_vec), dim3(256), 0, s, x, w, out, resid, size, eps, form);
+    else if (vpt == 2) hipLaunchKernelGGL(k_rmsnorm_v<2>, dim3(n_vec), dim3(256), 0, s, x, w, out, resid, size, eps, form);
+    else if (vpt <= 4) hipLaunchKernelGGL(k_rmsnorm_v<4>, dim3(n_vec), dim3(256), 0, s, x, w, out, resid, size, eps, form);
+    else hipLaunchKernelGGL(k_rmsnorm_v<8>, dim3(n_vec), dim3(256), 0, s, x, w, out, resid, size, eps, form);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(k_rmsnorm, dim3(n_vec), dim3(256), 0, s, x, w, out, resid, size, eps, form);
+  return hipGetLastError();
+}
+
+static int elementwise_blocks(int64_t n) {
+  int64_t b = (n + 255) / 256;
+  return (int)(b > 4096 ? 4096 : (b < 1 ? 1 : b));
+}
+
+hipError_t launch_add(float *x, const float *that, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_add, dim3(elementwise_blocks(n)), dim3(256), 0, s, x, that, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_softcap(float *v, int64_t n, float cap, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_softcap, dim3(elementwise_blocks(n)), dim3(256), 0, s, v, n, cap);
   return hipGetLastError();
 }
 

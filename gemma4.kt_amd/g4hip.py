@@ -107,6 +107,15 @@ SIGNATURES = {
     "g4_moe_route_dev": [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp],
     "g4_moe": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp],
     "g4_moe_dev": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp],
+    "g4_rmsnorm_dev": [_vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, ctypes.c_int],
+    "g4_rmsnorm_add_dev": [_vp, _vp, _vp, _vp, _i32, ctypes.c_float],
+    "g4_add_dev": [_vp, _vp, _vp, _i32],
+    "g4_softcap_dev": [_vp, _vp, _i32, ctypes.c_float],
+    "g4_matmul_norm_dev": [_vp, _vp, _i64, _vp, _vp, ctypes.c_float, _vp, _vp, _i32, _i32],
+    "g4_ffn_block": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float],
+    "g4_ffn_block_dev": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float],
+    "g4_lm_head": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, ctypes.c_float],
+    "g4_lm_head_dev": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, ctypes.c_float],
 }
 
 
@@ -447,3 +456,78 @@ def moe_dev(ctx: Context, gate_up, down, X, T: int, dim: int, ff: int, ids, weig
     check(lib().g4_moe_dev(ctx.handle, gate_up.handle, down.handle, _ptr(_dev_f32(X, "X")), int(T), int(dim),
                            int(ff), _ptr(ids), _ptr(_dev_f32(weights, "weights")), int(k),
                            _ptr(_dev_f32(Y, "Y"))))
+
+
+# ------------------------------------------------------------ decode step ---
+# The element-wise work around the matvec (Llama.kt:27-78 rmsnorm,
+# MutableFloatTensor.kt:28-37 addInPlace, Llama.kt:403-406 soft-capping) and the
+# blocks that keep the activations in device memory.  Norm weights are F32
+# tensors uploaded with FloatTensorFactory.create (ModelLoader.kt:281-286).
+
+NORM_WEIGHT_AFTER = 0   # Llama.kt:27-37: w * (s * x)
+NORM_WEIGHT_FIRST = 1   # Llama.kt:39-60: w * s * x
+NORM_NO_WEIGHT = 2      # Llama.kt:62-78: s * x
+
+
+def rmsnorm_dev(ctx: Context, weight: Optional[GpuFloatTensor], x, out, n_vec: int, size: int, eps: float,
+                form: int = NORM_WEIGHT_AFTER) -> None:
+    """n_vec vectors of `size` floats, each normalised on its own (out may be x)."""
+    check(lib().g4_rmsnorm_dev(ctx.handle, weight.handle if weight is not None else None, _ptr(_dev_f32(x, "x")),
+                               _ptr(_dev_f32(out, "out")), int(n_vec), int(size), float(eps), int(form)))
+
+
+def rmsnorm_add_dev(ctx: Context, weight: GpuFloatTensor, v, x, size: int, eps: float) -> None:
+    """v = rmsnorm(v); x += v (Llama.kt:222-223, 362-363)."""
+    check(lib().g4_rmsnorm_add_dev(ctx.handle, weight.handle, _ptr(_dev_f32(v, "v")), _ptr(_dev_f32(x, "x")),
+                                   int(size), float(eps)))
+
+
+def add_dev(ctx: Context, x, that, n: int) -> None:
+    """x += that (MutableFloatTensor.kt:28-37)."""
+    check(lib().g4_add_dev(ctx.handle, _ptr(_dev_f32(x, "x")), _ptr(_dev_f32(that, "that")), int(n)))
+
+
+def softcap_dev(ctx: Context, v, n: int, cap: float) -> None:
+    """v = cap * tanh(v / cap) (Llama.kt:403-406)."""
+    check(lib().g4_softcap_dev(ctx.handle, _ptr(_dev_f32(v, "v")), int(n), float(cap)))
+
+
+def matmul_norm_dev(ctx: Context, w: GpuFloatTensor, norm: GpuFloatTensor, x, out, dim0: int, dim1: int,
+                    eps: float, this_offset: int = 0, xnorm=None) -> None:
+    """out = W . rmsnorm(x, norm) with the norm fused into the matvec (Llama.kt:155-158)."""
+    check(lib().g4_matmul_norm_dev(ctx.handle, w.handle, int(this_offset), norm.handle, _ptr(_dev_f32(x, "x")),
+                                   float(eps), _ptr(_dev_f32(xnorm, "xnorm")), _ptr(_dev_f32(out, "out")),
+                                   int(dim0), int(dim1)))
+
+
+def ffn_block(ctx: Context, gate: GpuFloatTensor, up: GpuFloatTensor, down: GpuFloatTensor,
+              norm_pre: GpuFloatTensor, norm_post: GpuFloatTensor, x: np.ndarray, dim: int, hidden: int,
+              eps: float) -> np.ndarray:
+    """Dense FFN block of Llama.kt:355-363; returns the updated residual stream x."""
+    x = _f32(np.array(x, dtype=np.float32, copy=True), "x")
+    check(lib().g4_ffn_block(ctx.handle, gate.handle, up.handle, down.handle, norm_pre.handle, norm_post.handle,
+                             _ptr(x), int(dim), int(hidden), float(eps)))
+    return x
+
+
+def ffn_block_dev(ctx: Context, gate, up, down, norm_pre, norm_post, x, dim: int, hidden: int, eps: float) -> None:
+    check(lib().g4_ffn_block_dev(ctx.handle, gate.handle, up.handle, down.handle, norm_pre.handle,
+                                 norm_post.handle, _ptr(_dev_f32(x, "x")), int(dim), int(hidden), float(eps)))
+
+
+def lm_head(ctx: Context, w_cls: GpuFloatTensor, norm_final: GpuFloatTensor, x: np.ndarray, vocab: int, dim: int,
+            eps: float, softcap: float, want_logits: bool = True):
+    """Llama.kt:401-407 then Sampler.ARGMAX: (logits or None, index)."""
+    _f32(x, "x")
+    logits = np.empty(vocab, dtype=np.float32) if want_logits else None
+    idx = np.zeros(1, dtype=np.int32)
+    check(lib().g4_lm_head(ctx.handle, w_cls.handle, norm_final.handle, _ptr(x), _ptr(logits), _ptr(idx),
+                           int(vocab), int(dim), float(eps), float(softcap)))
+    return logits, int(idx[0])
+
+
+def lm_head_dev(ctx: Context, w_cls, norm_final, x, logits, index, vocab: int, dim: int, eps: float,
+                softcap: float, xnorm=None) -> None:
+    check(lib().g4_lm_head_dev(ctx.handle, w_cls.handle, norm_final.handle, _ptr(_dev_f32(x, "x")),
+                               _ptr(_dev_f32(xnorm, "xnorm")), _ptr(_dev_f32(logits, "logits")), _ptr(index),
+                               int(vocab), int(dim), float(eps), float(softcap)))

@@ -262,6 +262,33 @@ def q4_k_batched(m: int, seed: int = SEED_Q4_K_BATCHED, rows: int = 8192, cols: 
                 dim0=rows, dim1=cols, m=m)
 
 
+def norm_weight(seed: int, tag: str, n: int, scale: float = 1.0) -> np.ndarray:
+    """An F32 rms-norm weight: scale * (1 + N(0,1) / 4)."""
+    return (scale * (1.0 + 0.25 * normal(seed, tag, n))).astype(np.float32)
+
+
+RMS_EPS = 1e-6        # gemma4.attention.layer_norm_rms_epsilon default (ModelLoader.kt:59)
+LOGIT_SOFTCAP = 30.0  # a gemma4.final_logit_softcapping value (ModelLoader.kt:58)
+
+
+def q4_0_ffn_block(seed: int = SEED_Q4_0_FFN, dim: int = 2048, hidden: int = 8192) -> dict:
+    """The Q4_0 FFN above as a whole dense block (Llama.kt:355-363): the same
+    weights plus pre/post norm weights, and a residual stream x ~ N(0,1) * 4."""
+    d = q4_0_ffn(seed, dim, hidden)
+    d.update(norm_pre=norm_weight(seed, "norm_pre", dim), norm_post=norm_weight(seed, "norm_post", dim),
+             x=activations(seed, "x_resid", dim, 4.0), eps=RMS_EPS)
+    return d
+
+
+def q8_0_lm_head_block(seed: int = SEED_Q8_0_LM_HEAD, vocab: int = 262144, dim: int = 2048) -> dict:
+    """The Q8_0 LM head above behind its final norm and soft-cap (Llama.kt:401-407):
+    the same W and x, a final-norm weight of scale 0.05 (logits of standard
+    deviation about 3, below the cap of 30)."""
+    d = q8_0_lm_head(seed, vocab, dim)
+    d.update(norm=norm_weight(seed, "norm_final", dim, 0.05), eps=RMS_EPS, cap=LOGIT_SOFTCAP)
+    return d
+
+
 def moe_q4_k(tokens: int, seed: int = SEED_MOE_Q4_K, n_experts: int = 128, dim: int = 2048,
              ff: int = 1408, k: int = 8, routing_seed: int = 0) -> dict:
     """128 Q4_K experts (gate_up [E x 2ff x dim], down [E x dim x ff]), router

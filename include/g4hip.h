@@ -159,6 +159,50 @@ int g4_moe(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, con
 int g4_moe_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *d_X, int32_t T,
                int32_t dim, int32_t ff, const int32_t *d_ids, const float *d_weights, int32_t k, float *d_Y);
 
+/* ---- Decode step around the matvec: the activations stay in device memory. ----
+ * Norm weights are uploaded F32 tensors (ModelLoader.kt:281-286 reads norms as
+ * FloatBuffers and throws UnsupportedOperationException for any other type).
+ * s = (float)(1.0 / sqrt((double)(ss / size + eps))), ss = fp32 sum of x*x. */
+#define G4_NORM_WEIGHT_AFTER 0 /* Llama.kt:27-37 rmsnorm(out, x, weight, size, eps): w * (s * x) */
+#define G4_NORM_WEIGHT_FIRST 1 /* Llama.kt:39-60 rmsnorm(out, outOffset, x, xOffset, ...): w * s * x */
+#define G4_NORM_NO_WEIGHT 2    /* Llama.kt:62-78 rmsnormNoWeight: s * x */
+
+/* rms norm of n_vec vectors of `size` floats (vector v at d_x + v*size; the per-head
+ * q/k/v norms of Llama.kt:161-163, 185-188), each with its own scale and the shared
+ * weight (NULL for G4_NORM_NO_WEIGHT).  d_out may be d_x (in place). */
+int g4_rmsnorm_dev(g4_ctx *ctx, const g4_weight *weight, const float *d_x, float *d_out, int32_t n_vec, int32_t size,
+                   float eps, int form);
+/* Post-norm plus residual (Llama.kt:222-223, 362-363): v = rmsnorm(v) (the
+ * G4_NORM_WEIGHT_AFTER form, in place), then x += v.  One launch. */
+int g4_rmsnorm_add_dev(g4_ctx *ctx, const g4_weight *weight, float *d_v, float *d_x, int32_t size, float eps);
+/* MutableFloatTensor.kt:28-37 addInPlace: x[i] = x[i] + that[i]. */
+int g4_add_dev(g4_ctx *ctx, float *d_x, const float *d_that, int32_t n);
+/* Llama.kt:403-406 final logit soft-capping in place: v = cap * (float)tanh((double)(v / cap)), cap > 0. */
+int g4_softcap_dev(g4_ctx *ctx, float *d_v, int32_t n, float cap);
+/* Norm then matmul (Llama.kt:155-158: xb = rmsnorm(x, weight); W.matmul(xb, out, dim0, dim1)):
+ * out = W . rmsnorm(x) with the G4_NORM_WEIGHT_AFTER form fused into the matvec's
+ * staging of x.  d_xnorm (NULL, or not overlapping d_x) receives rmsnorm(x). */
+int g4_matmul_norm_dev(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const g4_weight *norm, const float *d_x,
+                       float eps, float *d_xnorm, float *d_out, int32_t dim0, int32_t dim1);
+/* Dense FFN block of one token, in place on x (Llama.kt:355-363):
+ *   xb = rmsnorm(x, norm_pre); h = gelu(w_gate xb) * (w_up xb); xb = rmsnorm(w_down h, norm_post); x += xb.
+ * Three launches: gate/up with the fused pre-norm, down, post-norm plus residual. */
+int g4_ffn_block(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const g4_weight *w_down,
+                 const g4_weight *norm_pre, const g4_weight *norm_post, float *x, int32_t dim, int32_t hidden,
+                 float eps);
+int g4_ffn_block_dev(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const g4_weight *w_down,
+                     const g4_weight *norm_pre, const g4_weight *norm_post, float *d_x, int32_t dim, int32_t hidden,
+                     float eps);
+/* Final norm, logits and greedy pick (Llama.kt:401-407, then Sampler.ARGMAX =
+ * FloatTensor.argmax, FloatTensor.kt:53-66):
+ *   logits = W_cls . rmsnorm(x, norm_final); if softcap > 0: logits = softcap(logits); index = argmax(logits).
+ * logits may be NULL; d_xnorm (device form, NULL or not overlapping d_x) receives
+ * rmsnorm(x), which the reference leaves in x. */
+int g4_lm_head(g4_ctx *ctx, const g4_weight *w_cls, const g4_weight *norm_final, const float *x, float *logits,
+               int32_t *index, int32_t vocab, int32_t dim, float eps, float softcap);
+int g4_lm_head_dev(g4_ctx *ctx, const g4_weight *w_cls, const g4_weight *norm_final, const float *d_x, float *d_xnorm,
+                   float *d_logits, int32_t *d_index, int32_t vocab, int32_t dim, float eps, float softcap);
+
 #ifdef __cplusplus
 }
 #endif

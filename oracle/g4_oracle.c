@@ -669,3 +669,158 @@ void or_moe_exact(int type_gu, const uint8_t *gate_up, int type_dn, const uint8_
   free(h);
   free(hb);
 }
+
+/* ---------------------------------------------------------- decode step --- */
+
+/* Llama.kt:27-78, the three rmsnorm forms.  ss is the sequential fp32 sum of
+ * x*x (FloatTensor.kt:31-37 reduce in the first form, an explicit loop in the
+ * others: the same roundings), then ss /= size, ss += eps and
+ * s = (float)(1.0 / sqrt((double)ss)).  out may alias x. */
+void or_rmsnorm(float *out, const float *x, const float *w, int32_t size, float eps, int form) {
+  float ss = 0.0f;
+  for (int32_t i = 0; i < size; i++) {
+    float xi = x[i];
+    ss = ss + xi * xi;
+  }
+  ss = ss / (float)size;
+  ss = ss + eps;
+  float s = (float)(1.0 / sqrt((double)ss));
+  for (int32_t i = 0; i < size; i++) {
+    if (form == OR_NORM_WEIGHT_AFTER) out[i] = w[i] * (s * x[i]); /* Llama.kt:33-36 */
+    else if (form == OR_NORM_WEIGHT_FIRST) out[i] = w[i] * s * x[i]; /* Llama.kt:56-58 */
+    else out[i] = s * x[i]; /* Llama.kt:75-77 */
+  }
+}
+
+/* fp64: s = 1/sqrt(sum x^2 / size + eps), out = w * s * x (w NULL: 1). */
+void or_rmsnorm_exact(double *out, const float *x, const float *w, int32_t size, float eps) {
+  double ss = 0.0;
+  for (int32_t i = 0; i < size; i++) ss += (double)x[i] * (double)x[i];
+  double s = 1.0 / sqrt(ss / (double)size + (double)eps);
+  for (int32_t i = 0; i < size; i++) out[i] = (w ? (double)w[i] : 1.0) * s * (double)x[i];
+}
+
+/* Llama.kt:403-406: cap * tanh((v / cap).toDouble()).toFloat(). */
+void or_softcap(float *v, int32_t n, float cap) {
+  for (int32_t i = 0; i < n; i++) {
+    float q = v[i] / cap;
+    float t = (float)tanh((double)q);
+    v[i] = cap * t;
+  }
+}
+
+/* Llama.kt:355-363 dense FFN block, in place on x. */
+void or_ffn_block(int type_g, const uint8_t *gate, int type_u, const uint8_t *up, int type_d, const uint8_t *down,
+                  const float *norm_pre, const float *norm_post, float *x, int32_t dim, int32_t hidden, float eps,
+                  int mode, int nthreads) {
+  float *xb = (float *)malloc(sizeof(float) * (size_t)dim);
+  float *hb = (float *)malloc(sizeof(float) * (size_t)hidden);
+  float *hb2 = (float *)malloc(sizeof(float) * (size_t)hidden);
+  or_rmsnorm(xb, x, norm_pre, dim, eps, OR_NORM_WEIGHT_AFTER);
+  or_matmul(type_g, gate, 0, xb, hb, hidden, dim, mode, nthreads);
+  or_matmul(type_u, up, 0, xb, hb2, hidden, dim, mode, nthreads);
+  for (int32_t i = 0; i < hidden; i++) hb[i] = or_gelu(hb[i]);
+  for (int32_t i = 0; i < hidden; i++) hb[i] = hb[i] * hb2[i];
+  or_matmul(type_d, down, 0, hb, xb, dim, hidden, mode, nthreads);
+  or_rmsnorm(xb, xb, norm_post, dim, eps, OR_NORM_WEIGHT_AFTER);
+  for (int32_t i = 0; i < dim; i++) x[i] = x[i] + xb[i];
+  free(xb);
+  free(hb);
+  free(hb2);
+}
+
+/* y = W x over fp64 inputs, with ya = sum |w x| and (bx != NULL) yb = sum |w| bx. */
+static void mv_exact64(int type, const uint8_t *raw, const double *x, const double *bx, double *y, double *ya,
+                       double *yb, int32_t dim0, int32_t dim1, int nthreads) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1)
+#endif
+  for (int32_t i = 0; i < dim0; i++) {
+    double s = 0.0, sa = 0.0, sb = 0.0;
+    const int64_t base = (int64_t)i * dim1;
+    for (int32_t j = 0; j < dim1; j++) {
+      double wv = (double)or_get(type, raw, base + j);
+      double p = wv * x[j];
+      s += p;
+      sa += fabs(p);
+      if (bx) sb += fabs(wv) * bx[j];
+    }
+    y[i] = s;
+    ya[i] = sa;
+    if (yb) yb[i] = sb;
+  }
+  (void)nthreads;
+}
+
+/* fp64 FFN block plus an error scale in units of 1e-5 (a check uses
+ * |x - x64| <= 1e-5 * bound64).  Budget: each rms scale is off by at most 1e-5
+ * relative, each dot by 1e-5 of its sum |w x|; the errors are carried through
+ * gelu (|gelu'| < 1.2), the product, the down projection, the post-norm (whose
+ * scale moves by sum |y| dy / (sum y^2 + dim eps)) and the residual add. */
+void or_ffn_block_exact(int type_g, const uint8_t *gate, int type_u, const uint8_t *up, int type_d,
+                        const uint8_t *down, const float *norm_pre, const float *norm_post, const float *x,
+                        double *x64, double *bound64, int32_t dim, int32_t hidden, float eps, int nthreads) {
+  double *xb = (double *)malloc(sizeof(double) * (size_t)dim);
+  double *bxb = (double *)malloc(sizeof(double) * (size_t)dim);
+  double *g = (double *)malloc(sizeof(double) * (size_t)hidden), *ag = (double *)malloc(sizeof(double) * (size_t)hidden);
+  double *u = (double *)malloc(sizeof(double) * (size_t)hidden), *au = (double *)malloc(sizeof(double) * (size_t)hidden);
+  double *h = (double *)malloc(sizeof(double) * (size_t)hidden), *bh = (double *)malloc(sizeof(double) * (size_t)hidden);
+  double *y = (double *)malloc(sizeof(double) * (size_t)dim), *ay = (double *)malloc(sizeof(double) * (size_t)dim);
+  double *by = (double *)malloc(sizeof(double) * (size_t)dim);
+  or_rmsnorm_exact(xb, x, norm_pre, dim, eps);
+  for (int32_t j = 0; j < dim; j++) bxb[j] = fabs(xb[j]);
+  mv_exact64(type_g, gate, xb, NULL, g, ag, NULL, hidden, dim, nthreads);
+  mv_exact64(type_u, up, xb, NULL, u, au, NULL, hidden, dim, nthreads);
+  for (int32_t i = 0; i < hidden; i++) {
+    double gi = g[i];
+    double gl = 0.5 * gi * (1.0 + tanh(sqrt(2.0 / 3.141592653589793) * (gi + 0.044715 * gi * gi * gi)));
+    h[i] = gl * u[i];
+    /* g and u are off by their dot error plus the carried norm error: 2 * sum |w xb| */
+    double bg = 2.0 * ag[i], bu = 2.0 * au[i];
+    bh[i] = 1.2 * bg * (fabs(u[i]) + 1e-5 * bu) + fabs(gl) * bu + 0.05 * fabs(h[i]);
+  }
+  mv_exact64(type_d, down, h, bh, y, ay, by, dim, hidden, nthreads);
+  double ss = 0.0, sdy = 0.0;
+  for (int32_t r = 0; r < dim; r++) {
+    by[r] += ay[r];
+    ss += y[r] * y[r];
+    sdy += fabs(y[r]) * by[r];
+  }
+  double s = 1.0 / sqrt(ss / (double)dim + (double)eps);
+  double rel_s = sdy / (ss + (double)dim * (double)eps) + 1.0;
+  for (int32_t r = 0; r < dim; r++) {
+    double z = (double)norm_post[r] * s * y[r];
+    double bz = fabs((double)norm_post[r]) * s * by[r] + fabs(z) * (rel_s + 0.05);
+    x64[r] = (double)x[r] + z;
+    bound64[r] = bz + 0.01 * fabs(x64[r]);
+  }
+  free(xb); free(bxb); free(g); free(ag); free(u); free(au); free(h); free(bh); free(y); free(ay); free(by);
+}
+
+/* Llama.kt:401-407 then Sampler.ARGMAX (FloatTensor.kt:53-66): logits =
+ * softcap(W rmsnorm(x)) (no cap when cap <= 0); returns the arg-max.  x is not
+ * modified (the reference normalises it in place). */
+int32_t or_lm_head(int type, const uint8_t *w, const float *norm, const float *x, float *logits, int32_t vocab,
+                   int32_t dim, float eps, float cap, int mode, int nthreads) {
+  float *xb = (float *)malloc(sizeof(float) * (size_t)dim);
+  or_rmsnorm(xb, x, norm, dim, eps, OR_NORM_WEIGHT_AFTER);
+  or_matmul(type, w, 0, xb, logits, vocab, dim, mode, nthreads);
+  if (cap > 0.0f) or_softcap(logits, vocab, cap);
+  free(xb);
+  return or_argmax(logits, 0, vocab);
+}
+
+/* fp64 logits plus error scale (units of 1e-5): the dot error plus the carried
+ * norm error (2 sum |w xb|); the cap has slope <= 1 and adds its roundings. */
+void or_lm_head_exact(int type, const uint8_t *w, const float *norm, const float *x, double *logits64,
+                      double *bound64, int32_t vocab, int32_t dim, float eps, float cap, int nthreads) {
+  double *xb = (double *)malloc(sizeof(double) * (size_t)dim);
+  or_rmsnorm_exact(xb, x, norm, dim, eps);
+  mv_exact64(type, w, xb, NULL, logits64, bound64, NULL, vocab, dim, nthreads);
+  for (int32_t i = 0; i < vocab; i++) {
+    bound64[i] *= 2.0;
+    if (cap > 0.0f) logits64[i] = (double)cap * tanh(logits64[i] / (double)cap);
+    bound64[i] += 0.05 * fabs(logits64[i]);
+  }
+  free(xb);
+}

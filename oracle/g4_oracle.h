@@ -117,6 +117,30 @@ void or_moe_exact(int type_gu, const uint8_t *gate_up, int type_dn, const uint8_
                   int32_t ff, const float *X, int32_t T, const int32_t *ids, const float *w, int32_t k,
                   double *Y64, double *bound64, int nthreads);
 
+/* ---- decode step ---- */
+/* rmsnorm forms: Llama.kt:27-37 w * (s * x); Llama.kt:39-60 w * s * x; Llama.kt:62-78 s * x. */
+enum { OR_NORM_WEIGHT_AFTER = 0, OR_NORM_WEIGHT_FIRST = 1, OR_NORM_NO_WEIGHT = 2 };
+/* s = (float)(1.0 / sqrt((double)(ss / size + eps))), ss the sequential fp32 sum of x*x.  out may alias x. */
+void or_rmsnorm(float *out, const float *x, const float *w, int32_t size, float eps, int form);
+/* fp64 rms norm (w NULL: no weight). */
+void or_rmsnorm_exact(double *out, const float *x, const float *w, int32_t size, float eps);
+/* Llama.kt:403-406 logit soft-capping in place. */
+void or_softcap(float *v, int32_t n, float cap);
+/* Llama.kt:355-363 dense FFN block in place on x (weights at offset 0). */
+void or_ffn_block(int type_g, const uint8_t *gate, int type_u, const uint8_t *up, int type_d, const uint8_t *down,
+                  const float *norm_pre, const float *norm_post, float *x, int32_t dim, int32_t hidden, float eps,
+                  int mode, int nthreads);
+/* fp64 FFN block and an error scale: a check uses |x - x64| <= 1e-5 * bound64. */
+void or_ffn_block_exact(int type_g, const uint8_t *gate, int type_u, const uint8_t *up, int type_d,
+                        const uint8_t *down, const float *norm_pre, const float *norm_post, const float *x,
+                        double *x64, double *bound64, int32_t dim, int32_t hidden, float eps, int nthreads);
+/* Llama.kt:401-407 + FloatTensor.kt:53-66: logits = softcap(W rmsnorm(x)) (cap <= 0: none); returns the arg-max. */
+int32_t or_lm_head(int type, const uint8_t *w, const float *norm, const float *x, float *logits, int32_t vocab,
+                   int32_t dim, float eps, float cap, int mode, int nthreads);
+/* fp64 logits and error scale (|logit - l64| <= 1e-5 * bound64). */
+void or_lm_head_exact(int type, const uint8_t *w, const float *norm, const float *x, double *logits64,
+                      double *bound64, int32_t vocab, int32_t dim, float eps, float cap, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,17 @@ _SIG = {
                 ctypes.c_int], None),
     "or_moe_exact": ([ctypes.c_int, _vp, ctypes.c_int, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _vp,
                       ctypes.c_int], None),
+    "or_rmsnorm": ([_vp, _vp, _vp, _i32, ctypes.c_float, ctypes.c_int], None),
+    "or_rmsnorm_exact": ([_vp, _vp, _vp, _i32, ctypes.c_float], None),
+    "or_softcap": ([_vp, _i32, ctypes.c_float], None),
+    "or_ffn_block": ([ctypes.c_int, _vp, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp, _vp, _vp, _i32, _i32,
+                      ctypes.c_float, ctypes.c_int, ctypes.c_int], None),
+    "or_ffn_block_exact": ([ctypes.c_int, _vp, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp,
+                            _i32, _i32, ctypes.c_float, ctypes.c_int], None),
+    "or_lm_head": ([ctypes.c_int, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, ctypes.c_float, ctypes.c_int,
+                    ctypes.c_int], _i32),
+    "or_lm_head_exact": ([ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, ctypes.c_float,
+                          ctypes.c_int], None),
 }
 
 _lib = None
@@ -232,3 +243,67 @@ def moe_exact(t_gu: int, gate_up, t_dn: int, down, X, ids, w, dim: int, ff: int,
     lib().or_moe_exact(t_gu, _p(gu), t_dn, _p(dn), dim, ff, _p(XX), T, _p(ii), _p(ww), k, _p(Y), _p(B),
                        threads or nthreads())
     return Y, B
+
+
+NORM_WEIGHT_AFTER, NORM_WEIGHT_FIRST, NORM_NO_WEIGHT = 0, 1, 2
+
+
+def rmsnorm(x, w, eps: float, form: int = NORM_WEIGHT_AFTER) -> np.ndarray:
+    """Llama.kt:27-78 over one vector (w may be None for NORM_NO_WEIGHT)."""
+    xx = _f(x)
+    ww = _f(w) if w is not None else None
+    out = np.empty(xx.size, dtype=np.float32)
+    lib().or_rmsnorm(_p(out), _p(xx), _p(ww) if ww is not None else None, xx.size, eps, form)
+    return out
+
+
+def rmsnorm_exact(x, w, eps: float) -> np.ndarray:
+    xx = _f(x)
+    ww = _f(w) if w is not None else None
+    out = np.empty(xx.size, dtype=np.float64)
+    lib().or_rmsnorm_exact(_p(out), _p(xx), _p(ww) if ww is not None else None, xx.size, eps)
+    return out
+
+
+def softcap(v, cap: float) -> np.ndarray:
+    vv = _f(v).copy()
+    lib().or_softcap(_p(vv), vv.size, cap)
+    return vv
+
+
+def ffn_block(t_g: int, gate, t_u: int, up, t_d: int, down, norm_pre, norm_post, x, dim: int, hidden: int,
+              eps: float, mode: int = MODE_VECTOR, threads: int = 0) -> np.ndarray:
+    g, u, d = _u8(gate), _u8(up), _u8(down)
+    npre, npost = _f(norm_pre), _f(norm_post)
+    xx = _f(x).copy()
+    lib().or_ffn_block(t_g, _p(g), t_u, _p(u), t_d, _p(d), _p(npre), _p(npost), _p(xx), dim, hidden, eps, mode,
+                       threads or nthreads())
+    return xx
+
+
+def ffn_block_exact(t_g: int, gate, t_u: int, up, t_d: int, down, norm_pre, norm_post, x, dim: int, hidden: int,
+                    eps: float, threads: int = 0):
+    g, u, d = _u8(gate), _u8(up), _u8(down)
+    npre, npost, xx = _f(norm_pre), _f(norm_post), _f(x)
+    x64 = np.empty(dim, dtype=np.float64)
+    b64 = np.empty(dim, dtype=np.float64)
+    lib().or_ffn_block_exact(t_g, _p(g), t_u, _p(u), t_d, _p(d), _p(npre), _p(npost), _p(xx), _p(x64), _p(b64),
+                             dim, hidden, eps, threads or nthreads())
+    return x64, b64
+
+
+def lm_head(t: int, raw, norm, x, vocab: int, dim: int, eps: float, cap: float, mode: int = MODE_VECTOR,
+            threads: int = 0):
+    r, nn, xx = _u8(raw), _f(norm), _f(x)
+    logits = np.empty(vocab, dtype=np.float32)
+    idx = lib().or_lm_head(t, _p(r), _p(nn), _p(xx), _p(logits), vocab, dim, eps, cap, mode, threads or nthreads())
+    return logits, idx
+
+
+def lm_head_exact(t: int, raw, norm, x, vocab: int, dim: int, eps: float, cap: float, threads: int = 0):
+    r, nn, xx = _u8(raw), _f(norm), _f(x)
+    l64 = np.empty(vocab, dtype=np.float64)
+    b64 = np.empty(vocab, dtype=np.float64)
+    lib().or_lm_head_exact(t, _p(r), _p(nn), _p(xx), _p(l64), _p(b64), vocab, dim, eps, cap,
+                           threads or nthreads())
+    return l64, b64

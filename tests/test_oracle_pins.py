@@ -371,3 +371,117 @@ def test_mutation_dropped_tail_detected(oracle):
     ex, a = oracle.exact_dot(Q8_0, raw, 7, x, 200)
     dropped, _ = oracle.exact_dot(Q8_0, raw, 7, x, 192)
     assert abs(dropped - ex) > 1e-5 * a
+
+
+# ---------------------------------------------------------- decode step ---
+# rmsnorm (Llama.kt:27-78), soft-capping (Llama.kt:403-406) and the blocks built
+# from them.  Pins: fp64 brute force with eps large enough to matter, closed forms
+# (constant vectors, unit mean square), exact power-of-two scale invariance, the
+# forms' product order on inputs whose sum of squares is exact, and the blocks
+# as compositions of the individually pinned functions.
+
+def _norm_inputs(n, seed=7):
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal(n).astype(np.float32), (1 + 0.25 * rng.standard_normal(n)).astype(np.float32)
+
+
+@pytest.mark.parametrize("eps", [1e-6, 0.1])
+@pytest.mark.parametrize("n", [1, 7, 256, 2048])
+def test_rmsnorm_vs_fp64(oracle, n, eps):
+    x, w = _norm_inputs(n)
+    exact = oracle.rmsnorm_exact(x, w, eps)
+    for form in (oracle.NORM_WEIGHT_AFTER, oracle.NORM_WEIGHT_FIRST):
+        got = oracle.rmsnorm(x, w, eps, form).astype(np.float64)
+        assert np.all(np.abs(got - exact) <= 1e-6 * np.abs(exact) + 1e-30), form
+    got = oracle.rmsnorm(x, None, eps, oracle.NORM_NO_WEIGHT).astype(np.float64)
+    ex = oracle.rmsnorm_exact(x, None, eps)
+    assert np.all(np.abs(got - ex) <= 1e-6 * np.abs(ex))
+    # eps sits inside the root, after the mean: moving it changes the result well past 1e-6
+    ss = float(np.sum(x.astype(np.float64) ** 2))
+    wrong = w * x / np.sqrt((ss + eps) / n)
+    assert n == 1 or eps < 0.01 or np.max(np.abs(wrong - exact) / np.abs(exact)) > 1e-3
+
+
+def test_rmsnorm_closed_forms(oracle):
+    # constant vector a: s = 1/sqrt(a^2 + eps) (the mean of equal squares is exact)
+    for a, eps in [(3.0, 0.0), (0.5, 1e-6), (1e-3, 1e-6)]:
+        x = np.full(64, a, np.float32)
+        got = oracle.rmsnorm(x, None, eps, oracle.NORM_NO_WEIGHT)
+        assert np.allclose(got, a / np.sqrt(np.float64(a) ** 2 + np.float64(np.float32(eps))), rtol=2e-7, atol=0)
+    # unit mean square without eps and weight
+    x, _ = _norm_inputs(2048, seed=3)
+    out = oracle.rmsnorm(x, None, 0.0, oracle.NORM_NO_WEIGHT).astype(np.float64)
+    assert abs(np.mean(out ** 2) - 1.0) < 1e-6
+    # scaling x by 2 scales ss by 4 and s by 1/2 exactly (eps = 0): same bits
+    w = _norm_inputs(2048, seed=4)[1]
+    assert same_bits(oracle.rmsnorm(2 * x, w, 0.0), oracle.rmsnorm(x, w, 0.0))
+
+
+def test_rmsnorm_form_order(oracle):
+    # integer x: every partial sum of squares is exact, so s is fixed and the
+    # forms differ only in the product order, which these inputs expose
+    rng = np.random.default_rng(11)
+    x = rng.integers(-64, 65, 2048).astype(np.float32)
+    w = (1 + 0.25 * rng.standard_normal(2048)).astype(np.float32)
+    ss = np.float32(np.sum(x.astype(np.float64) ** 2))  # exact: < 2^24
+    assert float(ss) == float(np.sum(x.astype(np.float64) ** 2))
+    s = np.float32(1.0 / np.sqrt(np.float64(np.float32(ss / np.float32(2048)) + np.float32(1e-6))))
+    after = oracle.rmsnorm(x, w, 1e-6, oracle.NORM_WEIGHT_AFTER)
+    first = oracle.rmsnorm(x, w, 1e-6, oracle.NORM_WEIGHT_FIRST)
+    assert same_bits(after, w * (s * x))
+    assert same_bits(first, (w * s) * x)
+    assert not same_bits(after, first)  # the order is observable on these inputs
+
+
+def test_softcap_properties(oracle):
+    cap = 30.0
+    v = np.concatenate([np.linspace(-200, 200, 40001), [0.0, 1e-30, 1e-3, 29.99, 1e9, -1e9]]).astype(np.float32)
+    c = oracle.softcap(v, cap)
+    assert np.all(np.abs(c) <= cap)
+    assert same_bits(oracle.softcap(-v, cap), -c)                 # odd
+    order = np.argsort(v, kind="stable")
+    assert np.all(np.diff(c[order].astype(np.float64)) >= 0)       # monotone
+    small = np.abs(v) < 1e-2
+    assert np.allclose(c[small], v[small], rtol=1e-6, atol=0)      # slope 1 at 0
+    ref = (cap * np.tanh(v.astype(np.float64) / cap)).astype(np.float32)
+    ulp = np.spacing(np.abs(ref).astype(np.float32))
+    assert np.all(np.abs(c.astype(np.float64) - ref) <= 2 * ulp)
+    assert same_bits(oracle.softcap(np.array([np.inf, -np.inf], np.float32), cap), np.array([cap, -cap], np.float32))
+    assert np.isnan(oracle.softcap(np.array([np.nan], np.float32), cap)[0])
+
+
+def test_ffn_block_is_the_composition(oracle):
+    dim, hidden, eps = 256, 512, 1e-6
+    g = synth.q4_0(5, "g", hidden * dim)
+    u = synth.q4_0(5, "u", hidden * dim)
+    d = synth.q4_0(5, "d", dim * hidden)
+    npre, npost = synth.norm_weight(5, "a", dim), synth.norm_weight(5, "b", dim)
+    x = synth.activations(5, "x", dim, 4.0)
+    got = oracle.ffn_block(Q4_0, g, Q4_0, u, Q4_0, d, npre, npost, x, dim, hidden, eps)
+    xb = oracle.rmsnorm(x, npre, eps)
+    h = np.array([oracle.gelu(float(v)) for v in oracle.matmul(Q4_0, g, xb, hidden, dim)], np.float32)
+    h = h * oracle.matmul(Q4_0, u, xb, hidden, dim)
+    y = oracle.rmsnorm(oracle.matmul(Q4_0, d, h, dim, hidden), npost, eps)
+    assert same_bits(got, x + y)
+    x64, b64 = oracle.ffn_block_exact(Q4_0, g, Q4_0, u, Q4_0, d, npre, npost, x, dim, hidden, eps)
+    assert np.all(np.abs(got - x64) <= 1e-5 * b64)
+    # swapping the two norm weights is caught by the bound
+    bad = oracle.ffn_block(Q4_0, g, Q4_0, u, Q4_0, d, npost, npre, x, dim, hidden, eps)
+    assert not np.all(np.abs(bad - x64) <= 1e-5 * b64)
+
+
+@pytest.mark.parametrize("cap", [0.0, 30.0])
+def test_lm_head_is_the_composition(oracle, cap):
+    vocab, dim, eps = 4096, 256, 1e-6
+    w = synth.q8_0(6, "w", vocab * dim, dscale=0.002)
+    norm = synth.norm_weight(6, "n", dim)
+    x = synth.activations(6, "x", dim)
+    logits, idx = oracle.lm_head(Q8_0, w, norm, x, vocab, dim, eps, cap)
+    ref = oracle.matmul(Q8_0, w, oracle.rmsnorm(x, norm, eps), vocab, dim)
+    if cap > 0:
+        ref = oracle.softcap(ref, cap)
+    assert same_bits(logits, ref)
+    assert idx == oracle.argmax(ref)
+    l64, b64 = oracle.lm_head_exact(Q8_0, w, norm, x, vocab, dim, eps, cap)
+    assert np.all(np.abs(logits - l64) <= 1e-5 * b64)
+    assert int(np.argmax(l64)) == idx
