@@ -374,7 +374,17 @@ class FloatTensorFactory:
     """FloatTensorFactory.kt:7-23: one tensor object per GGML type id."""
 
     @staticmethod
-    def create(ctx: Context, ggml_type: int, raw, n_elems: int) -> GpuFloatTensor:
+    def create(ctx: Context, ggml_type: int, raw, n_elems: Optional[int] = None) -> GpuFloatTensor:
+        """create(ctx, type, raw_bytes, n_elems), or create(ctx, type, entry) with a
+        GGMLTensorEntry of gguf.py (n_elems = the product of its shape, as
+        FloatTensorFactory.kt:8 computes it; the entry's mapped bytes are uploaded)."""
+        if n_elems is None:
+            if not hasattr(raw, "memory_segment"):
+                raise IllegalArgumentException("n_elems is required for raw bytes")
+            n = 1
+            for d in raw.shape:
+                n *= int(d)
+            return GpuFloatTensor(ctx, ggml_type, raw.memory_segment, n)
         return GpuFloatTensor(ctx, ggml_type, raw, n_elems)
 
 

@@ -322,3 +322,48 @@ def test_step_errors(g4, ctx, dev):
     out = dev.empty(64, dtype=dev.float32, device="cuda")
     with pytest.raises(g4.IllegalArgumentException):
         g4.matmul_norm_dev(ctx, w, nt, xd, out, 64, dim, 1e-6, xnorm=xd)
+
+
+# ------------------------------------------------------------ load hook ---
+
+def test_blocks_from_a_gguf_file(g4, ctx, oracle, tmp_path):
+    """The load hook end to end: tensors written to a GGUF file, parsed and mapped
+    (gguf.GGUF, GGUF.kt:195-212), uploaded through ModelLoader.load_quantized
+    (ModelLoader.kt:268-271 -> FloatTensorFactory.create), then the dense FFN block
+    and the LM-head tail run on the uploaded tensors with the file's eps and cap."""
+    import gguf
+    from gguf_writer import FLOAT32, STRING, write_gguf
+    announce("gguf load hook: ffn block + lm head from a file")
+    dim, hidden, vocab = 1024, 2816, 8192
+    src = {
+        "blk.0.ffn_gate.weight": ((dim, hidden), Q4_K, synth.q4_k(109, "g", hidden * dim)),
+        "blk.0.ffn_up.weight": ((dim, hidden), Q4_K, synth.q4_k(109, "u", hidden * dim)),
+        "blk.0.ffn_down.weight": ((hidden, dim), Q6_K, synth.q6_k(109, "d", dim * hidden)),
+        "blk.0.ffn_norm.weight": ((dim,), F32, synth.norm_weight(109, "n1", dim)),
+        "blk.0.post_ffw_norm.weight": ((dim,), F32, synth.norm_weight(109, "n2", dim)),
+        "output_norm.weight": ((dim,), F32, synth.norm_weight(109, "n3", dim, 0.05)),
+        "token_embd.weight": ((dim, vocab), Q8_0, synth.q8_0(109, "e", vocab * dim)),
+    }
+    path = str(tmp_path / "model.gguf")
+    write_gguf(path, [("general.architecture", STRING, "gemma4"),
+                      ("gemma4.attention.layer_norm_rms_epsilon", FLOAT32, 1e-6),
+                      ("gemma4.final_logit_softcapping", FLOAT32, 30.0)],
+               [(n, d, t, raw) for n, (d, t, raw) in src.items()], alignment=64)
+    g = gguf.GGUF.load_model(path)
+    entries = gguf.GGUF.load_tensors(path, g.tensor_data_offset, g.tensor_infos)
+    dv = {n: gguf.ModelLoader.load_quantized(ctx, e) for n, e in entries.items()}
+    eps = g.metadata["gemma4.attention.layer_norm_rms_epsilon"]
+    cap = g.metadata["gemma4.final_logit_softcapping"]
+    for n, (d, t, raw) in src.items():
+        assert dv[n].size == int(np.prod(d)) and dv[n].nbytes == raw.nbytes
+    r = {n: raw for n, (d, t, raw) in src.items()}
+    x = synth.activations(109, "x", dim, 4.0)
+    x1 = g4.ffn_block(ctx, dv["blk.0.ffn_gate.weight"], dv["blk.0.ffn_up.weight"], dv["blk.0.ffn_down.weight"],
+                      dv["blk.0.ffn_norm.weight"], dv["blk.0.post_ffw_norm.weight"], x, dim, hidden, eps)
+    x64, b64 = oracle.ffn_block_exact(Q4_K, r["blk.0.ffn_gate.weight"], Q4_K, r["blk.0.ffn_up.weight"], Q6_K,
+                                      r["blk.0.ffn_down.weight"], r["blk.0.ffn_norm.weight"],
+                                      r["blk.0.post_ffw_norm.weight"], x, dim, hidden, eps)
+    within(x1, x64, TOL * b64, "ffn block from gguf")
+    logits, idx = g4.lm_head(ctx, dv["token_embd.weight"], dv["output_norm.weight"], x1, vocab, dim, eps, cap)
+    l64, lb = oracle.lm_head_exact(Q8_0, r["token_embd.weight"], r["output_norm.weight"], x1, vocab, dim, eps, cap)
+    _lm_check(logits, idx, l64, lb, "lm head from gguf")
