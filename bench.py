@@ -18,7 +18,8 @@ cores over a bounded sample of the same workload.
 Other workloads: --workload q8_0_matvec | q4_0_ffn | q8_0_lm_head |
 q4_k_batched[:M] | moe[:T] | q5_k_matvec | q6_k_matvec | q4_0_ffn_block (the
 FFN with its norms and residual add) | q8_0_lm_head_cap (final norm, soft-cap,
-arg-max); --all prints one line per workload.
+arg-max) | attention[:L] (decode attention over L cached positions); --all prints
+one line per workload.
 """
 from __future__ import annotations
 
@@ -427,6 +428,47 @@ class LmHeadCapQ8_0(LmHeadQ8_0):
                 "softcap": self.cap, "algorithmic_bytes_per_step": self.step_bytes, "weight_copies": self.copies}
 
 
+class AttentionDecode(Workload):
+    """Decode attention of one token over one layer's KV cache (Llama.kt:198-218):
+    16 query heads sharing 8 kv heads of size 256, fp32 caches of `length` rows."""
+    dominant_name = "k_att_part<256, 2> + k_att_combine"
+
+    def __init__(self, g4, ctx, torch, length: int):
+        import synth
+        self.H, self.KV, self.HS, self.Lc = 16, 8, 256, length
+        kv_dim = self.KV * self.HS
+        self.name = "attention_decode_h16_kv8_d256_len%d" % length
+        self.q_np = synth.activations(0xA77, "q", self.H * self.HS)
+        self.k_np = synth.activations(0xA77, "k", length * kv_dim)
+        self.v_np = synth.activations(0xA77, "v", length * kv_dim)
+        cache_bytes = 2 * self.k_np.nbytes
+        self.copies = copies_for(cache_bytes, cap=64)
+        self.q = torch.from_numpy(self.q_np).cuda()
+        self.kc = [torch.from_numpy(self.k_np).cuda() for _ in range(self.copies)]
+        self.vc = [torch.from_numpy(self.v_np).cuda() for _ in range(self.copies)]
+        self.out = torch.empty(self.H * self.HS, dtype=torch.float32, device="cuda")
+        # K and V rows once each, q read, out written
+        self.step_bytes = cache_bytes + 2 * 4 * self.H * self.HS
+        self.dominant_bytes = self.step_bytes
+        self.g4, self.ctx = g4, ctx
+
+    def step(self, i):
+        c = i % self.copies
+        self.g4.attention_dev(self.ctx, self.q, self.kc[c], self.vc[c], self.out, self.H, self.KV, self.HS,
+                              self.Lc - 1, 0)
+
+    def cpu_setup(self, oracle):
+        self.oracle = oracle
+
+    def cpu_step(self):
+        self.oracle.attention(self.q_np, self.k_np, self.v_np, self.H, self.KV, self.HS, self.Lc - 1, 0)
+
+    def config(self):
+        return {"workload": self.name, "n_heads": self.H, "n_kv_heads": self.KV, "head_size": self.HS,
+                "positions": self.Lc, "cache": "fp32", "algorithmic_bytes_per_step": self.step_bytes,
+                "cache_copies": self.copies}
+
+
 class CopyCalibration(Workload):
     """A plain fp32 copy of known size (y = x * 1 through torch's elementwise kernel).
 
@@ -464,6 +506,8 @@ def make_workload(spec: str, g4, ctx, torch) -> Workload:
         return FfnBlockQ4_0(g4, ctx, torch)
     if name == "q8_0_lm_head_cap":
         return LmHeadCapQ8_0(g4, ctx, torch)
+    if name == "attention":
+        return AttentionDecode(g4, ctx, torch, int(arg or 8192))
     if name == "q4_k_batched":
         return BatchedQ4_K(g4, ctx, torch, int(arg or 8))
     if name == "moe":
@@ -624,7 +668,7 @@ def main():
     if args.all:
         specs = ["q4_0_ffn", "q8_0_matvec", "q8_0_lm_head", "q4_k_batched:1", "q4_k_batched:8",
                  "q4_k_batched:32", "q4_k_batched:64", "moe:1", "moe:16", "q5_k_matvec", "q6_k_matvec",
-                 "q4_0_ffn_block", "q8_0_lm_head_cap"]
+                 "q4_0_ffn_block", "q8_0_lm_head_cap", "attention:8192"]
     for s in specs:
         line = run(s, args.steps, args.warmup, args.cpu_seconds, not args.eager)
         print(json.dumps(line), flush=True)

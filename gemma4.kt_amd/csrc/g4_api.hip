@@ -1136,4 +1136,40 @@ int g4_lm_head_dev(g4_ctx *ctx, const g4_weight *w_cls, const g4_weight *norm_fi
                          (float *)(ctx->scratch + on), nullptr, d_index, softcap);
 }
 
+// ------------------------------------------------------------ attention ----
+
+int g4_attention_dev(g4_ctx *ctx, const float *d_q, const float *d_key_cache, const float *d_value_cache,
+                     float *d_out, int32_t n_heads, int32_t n_kv_heads, int32_t head_size, int32_t position,
+                     int32_t att_start) {
+  G4_TRY(check_ctx(ctx));
+  if (n_heads <= 0 || n_kv_heads <= 0 || head_size <= 0)
+    return fail(G4_ERR_INVALID_ARGUMENT, "heads and head size must be positive (%d, %d, %d)", n_heads, n_kv_heads,
+                head_size);
+  if (n_heads % n_kv_heads != 0)
+    return fail(G4_ERR_INVALID_ARGUMENT, "n_heads %d is not a multiple of n_kv_heads %d", n_heads, n_kv_heads);
+  if (att_start < 0 || position < att_start)
+    return fail(G4_ERR_OUT_OF_RANGE, "positions %d..%d", att_start, position);
+  if ((int64_t)n_kv_heads * head_size > 0x7fffffff) return fail(G4_ERR_INVALID_ARGUMENT, "kv_dim too large");
+  if (!d_q || !d_key_cache || !d_value_cache || !d_out) return fail(G4_ERR_INVALID_ARGUMENT, "null pointer");
+  G4_TRY(use_device(ctx));
+  g4::AttArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = d_q;
+  a.kc = d_key_cache;
+  a.vc = d_value_cache;
+  a.out = d_out;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv_heads;
+  a.hs = head_size;
+  a.row0 = att_start;
+  a.rows = position - att_start + 1;
+  // the vector kernel reads 16-byte words: caches, q and out must be 16-byte aligned
+  a.generic = ((uintptr_t)d_q | (uintptr_t)d_key_cache | (uintptr_t)d_value_cache | (uintptr_t)d_out) % 16 != 0;
+  g4::attention_plan(a, ctx->dev);
+  Carve c;
+  size_t o = c.add(sizeof(float) * (size_t)g4::attention_scratch_floats(a));
+  G4_TRY(ensure_scratch(ctx, c.off));
+  return launch_status(g4::launch_attention(a, (float *)(ctx->scratch + o), ctx->stream), "attention");
+}
+
 }  // extern "C"

@@ -102,4 +102,31 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float *out, float *res
 hipError_t launch_add(float *x, const float *that, int64_t n, hipStream_t stream);
 hipError_t launch_softcap(float *v, int64_t n, float cap, hipStream_t stream);
 
+// Decode attention over a layer's KV cache (Llama.kt:198-218).  Rows row0 ..
+// row0 + rows - 1 of the caches; head h reads kv head h / kv_mul.  attention_plan
+// fills kv_mul, n_groups, ch and n_chunks; the launch needs
+// attention_scratch_floats() floats of scratch (16-byte aligned).
+struct AttArgs {
+  const float *q;
+  const float *kc;
+  const float *vc;
+  float *out;
+  float *part;
+  float *ml;
+  int32_t n_heads;
+  int32_t n_kv;
+  int32_t hs;
+  int32_t kv_mul;
+  int32_t n_groups;
+  int32_t row0;
+  int32_t rows;
+  int32_t ch;
+  int32_t n_chunks;
+  int32_t generic;  // 1: one workgroup per head (any head size or alignment); set before attention_plan
+};
+bool attention_fast_ok(int32_t hs);
+void attention_plan(AttArgs &a, const DevInfo &dev);
+int64_t attention_scratch_floats(const AttArgs &a);
+hipError_t launch_attention(AttArgs a, float *scratch, hipStream_t stream);
+
 }  // namespace g4

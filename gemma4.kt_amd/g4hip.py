@@ -116,6 +116,7 @@ SIGNATURES = {
     "g4_ffn_block_dev": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float],
     "g4_lm_head": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, ctypes.c_float],
     "g4_lm_head_dev": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, ctypes.c_float],
+    "g4_attention_dev": [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32],
 }
 
 
@@ -541,3 +542,11 @@ def lm_head_dev(ctx: Context, w_cls, norm_final, x, logits, index, vocab: int, d
     check(lib().g4_lm_head_dev(ctx.handle, w_cls.handle, norm_final.handle, _ptr(_dev_f32(x, "x")),
                                _ptr(_dev_f32(xnorm, "xnorm")), _ptr(_dev_f32(logits, "logits")), _ptr(index),
                                int(vocab), int(dim), float(eps), float(softcap)))
+
+
+def attention_dev(ctx: Context, q, key_cache, value_cache, out, n_heads: int, n_kv_heads: int, head_size: int,
+                  position: int, att_start: int = 0) -> None:
+    """Decode attention over one layer's KV cache (Llama.kt:198-218); device tensors."""
+    check(lib().g4_attention_dev(ctx.handle, _ptr(_dev_f32(q, "q")), _ptr(_dev_f32(key_cache, "key_cache")),
+                                 _ptr(_dev_f32(value_cache, "value_cache")), _ptr(_dev_f32(out, "out")),
+                                 int(n_heads), int(n_kv_heads), int(head_size), int(position), int(att_start)))

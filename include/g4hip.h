@@ -203,6 +203,20 @@ int g4_lm_head(g4_ctx *ctx, const g4_weight *w_cls, const g4_weight *norm_final,
 int g4_lm_head_dev(g4_ctx *ctx, const g4_weight *w_cls, const g4_weight *norm_final, const float *d_x, float *d_xnorm,
                    float *d_logits, int32_t *d_index, int32_t vocab, int32_t dim, float eps, float softcap);
 
+/* Decode attention of one token over one layer's KV cache (Llama.kt:198-218):
+ *   for each query head h (kv head h / (n_heads / n_kv_heads)), scores
+ *   s_t = q_h . K[t] with scale 1 for t = att_start..position, softmax
+ *   (MutableFloatTensor.kt:54-59: max, exp in double), out_h = sum_t a_t V[t].
+ * d_q, d_out: [n_heads x head_size]; d_key_cache, d_value_cache: fp32 rows of
+ * kv_dim = n_kv_heads * head_size floats, row t at t * kv_dim, holding at least
+ * position + 1 rows.  att_start = max(0, position - window + 1) on sliding-window
+ * layers, 0 otherwise (Llama.kt:197).  Head sizes 64/128/256/512 with 16-byte
+ * aligned buffers take the split-sequence kernel (two launches); any other shape
+ * takes a one-workgroup-per-head kernel. */
+int g4_attention_dev(g4_ctx *ctx, const float *d_q, const float *d_key_cache, const float *d_value_cache,
+                     float *d_out, int32_t n_heads, int32_t n_kv_heads, int32_t head_size, int32_t position,
+                     int32_t att_start);
+
 #ifdef __cplusplus
 }
 #endif

@@ -824,3 +824,88 @@ void or_lm_head_exact(int type, const uint8_t *w, const float *norm, const float
   }
   free(xb);
 }
+
+/* ------------------------------------------------------------ attention --- */
+
+/* ArrayFloatTensor.kt:66-88 vectorDot of two float arrays (512-bit species):
+ * 16-lane fma accumulation, reduceLanes, then the scalar tail. */
+static float array_vdot(const float *a, const float *b, int32_t n) {
+  float acc[16] = {0};
+  int32_t ub = n & ~15;
+  for (int32_t i = 0; i < ub; i += 16)
+    for (int l = 0; l < 16; l++) acc[l] = fmaf(a[i + l], b[i + l], acc[l]);
+  float r = reduce16(acc);
+  for (int32_t i = ub; i < n; i++) r += a[i] * b[i];
+  return r;
+}
+
+/* Llama.kt:198-218 for every head of one layer at one position: scores
+ * q_h . K[t] (scale 1) for t in att_start..position, softmaxInPlace, then
+ * out_h = sum_t a_t V[t] as saxpyInPlace in t order.  Head h reads kv head
+ * h / (n_heads / n_kv); row t of a cache starts at t * n_kv * hs. */
+void or_attention(const float *q, const float *kc, const float *vc, float *out, int32_t n_heads, int32_t n_kv,
+                  int32_t hs, int32_t position, int32_t att_start) {
+  const int32_t kv_dim = n_kv * hs, kv_mul = n_heads / n_kv, L = position - att_start + 1;
+  float *att = (float *)malloc(sizeof(float) * (size_t)(L > 0 ? L : 1));
+  for (int32_t h = 0; h < n_heads; h++) {
+    const int32_t kvh = h / kv_mul;
+    for (int32_t t = att_start; t <= position; t++)
+      att[t - att_start] = array_vdot(q + (size_t)h * hs, kc + (size_t)t * kv_dim + (size_t)kvh * hs, hs);
+    or_softmax(att, 0, L);
+    float *o = out + (size_t)h * hs;
+    for (int32_t i = 0; i < hs; i++) o[i] = 0.0f;
+    for (int32_t t = att_start; t <= position; t++) {
+      const float a = att[t - att_start];
+      const float *v = vc + (size_t)t * kv_dim + (size_t)kvh * hs;
+      for (int32_t i = 0; i < hs; i++) o[i] = a * v[i] + o[i];
+    }
+  }
+  free(att);
+}
+
+/* fp64 attention plus an error scale in units of 1e-5 (|out - out64| <= 1e-5 *
+ * bound64): each score may be off by 1e-5 of its sum |q k|, which moves each
+ * softmax weight by at most 2 max_t(error) of itself; the weighted sums add
+ * rounding of a few units of 1e-5 of sum a |v|. */
+void or_attention_exact(const float *q, const float *kc, const float *vc, double *out64, double *bound64,
+                        int32_t n_heads, int32_t n_kv, int32_t hs, int32_t position, int32_t att_start,
+                        int nthreads) {
+  const int32_t kv_dim = n_kv * hs, kv_mul = n_heads / n_kv, L = position - att_start + 1;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1)
+#endif
+  for (int32_t h = 0; h < n_heads; h++) {
+    const int32_t kvh = h / kv_mul;
+    double *s = (double *)malloc(sizeof(double) * (size_t)L);
+    double smax = -INFINITY, amax = 0.0;
+    for (int32_t t = 0; t < L; t++) {
+      const float *k = kc + (size_t)(att_start + t) * kv_dim + (size_t)kvh * hs;
+      double d = 0.0, a = 0.0;
+      for (int32_t i = 0; i < hs; i++) {
+        double p = (double)q[(size_t)h * hs + i] * (double)k[i];
+        d += p;
+        a += fabs(p);
+      }
+      s[t] = d;
+      if (d > smax) smax = d;
+      if (a > amax) amax = a;
+    }
+    double sum = 0.0;
+    for (int32_t t = 0; t < L; t++) {
+      s[t] = exp(s[t] - smax);
+      sum += s[t];
+    }
+    for (int32_t i = 0; i < hs; i++) {
+      double o = 0.0, oa = 0.0;
+      for (int32_t t = 0; t < L; t++) {
+        const double v = (double)vc[(size_t)(att_start + t) * kv_dim + (size_t)kvh * hs + i];
+        o += s[t] * v;
+        oa += s[t] * fabs(v);
+      }
+      out64[(size_t)h * hs + i] = o / sum;
+      bound64[(size_t)h * hs + i] = (2.0 * amax + 5.0) * oa / sum;
+    }
+    free(s);
+  }
+  (void)nthreads;
+}

@@ -141,6 +141,16 @@ int32_t or_lm_head(int type, const uint8_t *w, const float *norm, const float *x
 void or_lm_head_exact(int type, const uint8_t *w, const float *norm, const float *x, double *logits64,
                       double *bound64, int32_t vocab, int32_t dim, float eps, float cap, int nthreads);
 
+/* Llama.kt:198-218: decode attention of every head over the KV cache rows
+ * att_start..position (scale 1, head h reads kv head h / (n_heads / n_kv), row t
+ * of a cache at t * n_kv * hs). */
+void or_attention(const float *q, const float *kc, const float *vc, float *out, int32_t n_heads, int32_t n_kv,
+                  int32_t hs, int32_t position, int32_t att_start);
+/* fp64 attention and error scale (|out - out64| <= 1e-5 * bound64). */
+void or_attention_exact(const float *q, const float *kc, const float *vc, double *out64, double *bound64,
+                        int32_t n_heads, int32_t n_kv, int32_t hs, int32_t position, int32_t att_start,
+                        int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,8 @@ _SIG = {
                     ctypes.c_int], _i32),
     "or_lm_head_exact": ([ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, ctypes.c_float,
                           ctypes.c_int], None),
+    "or_attention": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32], None),
+    "or_attention_exact": ([_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, ctypes.c_int], None),
 }
 
 _lib = None
@@ -307,3 +309,21 @@ def lm_head_exact(t: int, raw, norm, x, vocab: int, dim: int, eps: float, cap: f
     lib().or_lm_head_exact(t, _p(r), _p(nn), _p(xx), _p(l64), _p(b64), vocab, dim, eps, cap,
                            threads or nthreads())
     return l64, b64
+
+
+def attention(q, kc, vc, n_heads: int, n_kv: int, hs: int, position: int, att_start: int = 0) -> np.ndarray:
+    """Llama.kt:198-218 for one layer at one position: out [n_heads x hs]."""
+    qq, kk, vv = _f(q), _f(kc), _f(vc)
+    out = np.empty(n_heads * hs, dtype=np.float32)
+    lib().or_attention(_p(qq), _p(kk), _p(vv), _p(out), n_heads, n_kv, hs, position, att_start)
+    return out.reshape(n_heads, hs)
+
+
+def attention_exact(q, kc, vc, n_heads: int, n_kv: int, hs: int, position: int, att_start: int = 0,
+                    threads: int = 0):
+    qq, kk, vv = _f(q), _f(kc), _f(vc)
+    o = np.empty(n_heads * hs, dtype=np.float64)
+    b = np.empty(n_heads * hs, dtype=np.float64)
+    lib().or_attention_exact(_p(qq), _p(kk), _p(vv), _p(o), _p(b), n_heads, n_kv, hs, position, att_start,
+                             threads or nthreads())
+    return o.reshape(n_heads, hs), b.reshape(n_heads, hs)

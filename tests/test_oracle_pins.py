@@ -485,3 +485,60 @@ def test_lm_head_is_the_composition(oracle, cap):
     l64, b64 = oracle.lm_head_exact(Q8_0, w, norm, x, vocab, dim, eps, cap)
     assert np.all(np.abs(logits - l64) <= 1e-5 * b64)
     assert int(np.argmax(l64)) == idx
+
+
+# ------------------------------------------------------------ attention ---
+# Llama.kt:198-218.  Pins: a single position returns V exactly; equal keys give
+# the mean of V; GQA reads kv head h / kv_mul; rows before the window start are
+# never read; fp64 brute force within the propagated bound.
+
+def _att_inputs(n_heads, n_kv, hs, rows, seed=21):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal(n_heads * hs).astype(np.float32)
+    kc = rng.standard_normal(rows * n_kv * hs).astype(np.float32)
+    vc = rng.standard_normal(rows * n_kv * hs).astype(np.float32)
+    return q, kc, vc
+
+
+def test_attention_single_position_returns_v(oracle):
+    q, kc, vc = _att_inputs(4, 2, 64, 1)
+    out = oracle.attention(q, kc, vc, 4, 2, 64, 0)
+    v = vc.reshape(1, 2, 64)[0]
+    assert same_bits(out, np.stack([v[0], v[0], v[1], v[1]]))
+
+
+def test_attention_equal_keys_average_v(oracle):
+    n_heads, n_kv, hs, rows = 2, 1, 32, 100
+    q, _, vc = _att_inputs(n_heads, n_kv, hs, rows)
+    kc = np.tile(np.random.default_rng(3).standard_normal(hs).astype(np.float32), rows)
+    out = oracle.attention(q, kc, vc, n_heads, n_kv, hs, rows - 1)
+    mean = vc.reshape(rows, hs).astype(np.float64).mean(axis=0)
+    assert np.allclose(out, mean, rtol=0, atol=1e-5)
+
+
+def test_attention_gqa_mapping_and_window(oracle):
+    n_heads, n_kv, hs, rows = 8, 2, 64, 50
+    q, kc, vc = _att_inputs(n_heads, n_kv, hs, rows)
+    v = vc.reshape(rows, n_kv, hs)
+    v[:, 0, :] = 1.0
+    v[:, 1, :] = 2.0
+    kc.reshape(rows, n_kv, hs)[:20] = np.nan  # before the window: never read
+    v[:20] = np.nan
+    out = oracle.attention(q, kc, v.reshape(-1), n_heads, n_kv, hs, rows - 1, 20)
+    want = np.repeat([1.0, 2.0], n_heads // n_kv)[:, None] * np.ones(hs)
+    assert np.allclose(out, want, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hs,rows,start", [(4, 4, 64, 37, 0), (8, 2, 256, 300, 0),
+                                                        (8, 1, 128, 500, 250), (2, 1, 80, 64, 10)])
+def test_attention_vs_fp64(oracle, n_heads, n_kv, hs, rows, start):
+    q, kc, vc = _att_inputs(n_heads, n_kv, hs, rows)
+    out = oracle.attention(q, kc, vc, n_heads, n_kv, hs, rows - 1, start)
+    o64, b64 = oracle.attention_exact(q, kc, vc, n_heads, n_kv, hs, rows - 1, start)
+    assert np.all(np.abs(out - o64) <= 1e-5 * b64)
+    # the bound is not vacuous: reading kv head h % n_kv instead breaks it when heads share kv heads
+    if n_heads != n_kv and n_kv > 1:
+        bad = np.stack([oracle.attention(q[h * hs:(h + 1) * hs], np.ascontiguousarray(
+            kc.reshape(rows, n_kv, hs)[:, h % n_kv]), np.ascontiguousarray(vc.reshape(rows, n_kv, hs)[:, h % n_kv]),
+            1, 1, hs, rows - 1, start)[0] for h in range(n_heads)])
+        assert not np.all(np.abs(bad - o64) <= 1e-5 * b64)
