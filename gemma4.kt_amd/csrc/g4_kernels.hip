@@ -18,6 +18,11 @@
 #include "g4_device.hpp"
 #include "g4_internal.hpp"
 
+// Target tiles per wave of a row launch (one computing while the next is in flight).
+#ifndef G4_TILES_PER_WAVE
+#define G4_TILES_PER_WAVE 2
+#endif
+
 namespace g4 {
 
 static_assert(NORM_WEIGHT_AFTER == G4_NORM_WEIGHT_AFTER && NORM_WEIGHT_FIRST == G4_NORM_WEIGHT_FIRST &&
@@ -51,11 +56,24 @@ __device__ void am_partial(float v, int i, float *pv, int32_t *pi) {
   if (threadIdx.x == 0) pv[blockIdx.x] = v, pi[blockIdx.x] = i;
 }
 
-// One 256-thread block: best of n block partials -> *out.
+// One 256-thread block: best of n block partials -> *out.  The first 2048
+// partials are loaded before any comparison (one round trip to memory).
 __global__ __launch_bounds__(256) void k_argmax_final(const float *pv, const int32_t *pi, int n, int32_t *out) {
+  constexpr int U = 8;
   float v = -__builtin_inff();
   int i = INT_MAX;
-  for (int b = threadIdx.x; b < n; b += 256)
+  float cv[U];
+  int ci[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int b = threadIdx.x + 256 * u;
+    cv[u] = pv[b < n ? b : 0];
+    ci[u] = pi[b < n ? b : 0];
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (threadIdx.x + 256 * u < n && am_better(cv[u], ci[u], v, i)) v = cv[u], i = ci[u];
+  for (int b = threadIdx.x + 256 * U; b < n; b += 256)
     if (am_better(pv[b], pi[b], v, i)) v = pv[b], i = pi[b];
   am_block(v, i);
   if (threadIdx.x == 0) *out = i;
@@ -312,7 +330,26 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     }
   }
 
-  if constexpr (EPI == EPI_GELU_PAIR) gq_flush();
+  if constexpr (EPI == EPI_GELU_PAIR) {
+    // The rows still queued when the tiles run out: when the four waves' rows
+    // fit in 64 lanes, one wave evaluates them all (one double-precision gelu
+    // pass per workgroup instead of one per wave at the kernel's tail).
+    __shared__ int gq_meta[4][2];
+    if (lane == 0) gq_meta[wid][0] = gq_n, gq_meta[wid][1] = gq_row;
+    __syncthreads();
+    const int tot = gq_meta[0][0] + gq_meta[1][0] + gq_meta[2][0] + gq_meta[3][0];
+    if (tot <= 64) {
+      if (wid == 0 && lane < tot) {
+        int w = 0, k = lane;
+        while (k >= gq_meta[w][0]) k -= gq_meta[w][0], ++w;
+        const float2 p = gq[w][k];
+        const int lr = gq_meta[w][1] + k;
+        if (lr < a.rows) y[lr] = gelu_ref(p.x) * p.y;
+      }
+    } else {
+      gq_flush();
+    }
+  }
   if constexpr (AQ) aq_flush();
   if constexpr (EPI == EPI_ARGMAX) am_partial(best_v, best_i, a.am_val, a.am_idx);
 }
@@ -613,9 +650,12 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
   // workgroup per CU over all segments (a partial round leaves CUs with half
   // the work of the others), at most what is resident at once, never more
   // workgroups than tiles (idle waves only help stage x).
-  int64_t blocks = (n_tiles + 7) / 8;
+  int64_t blocks = (n_tiles + 4 * G4_TILES_PER_WAVE - 1) / (4 * G4_TILES_PER_WAVE);
   blocks = ((blocks * segs + cu - 1) / cu * cu + segs - 1) / segs;
-  const int64_t cap = cu * res / segs;
+  // at most two resident workgroups per CU: with more requests in flight a long
+  // stream (the 570 MB LM head) was measured slower, and the small launches
+  // never reach the cap
+  const int64_t cap = cu * (res < 2 ? res : 2) / segs;
   if (blocks > cap) blocks = cap;
   if (blocks > n_tiles) blocks = n_tiles;
   if (blocks < 1) blocks = 1;
