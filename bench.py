@@ -37,6 +37,7 @@ import numpy as np  # noqa: E402
 
 METRIC = "quant matvec GB/s & % of HBM peak (Q8_0/Q4_0/Q4_K); MoE expert tokens/s"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 matrix-core peak
 MALL_BYTES = 256 << 20
 Q8_0, Q4_0, Q4_K = 8, 2, 12
 
@@ -46,14 +47,20 @@ Q8_0, Q4_0, Q4_K = 8, 2, 12
 # (KiB), the factors being what the counters read for a plain 256 MiB fp32 copy.
 # Recorded in profiles/hbm_traffic_fetch_write_size.md (same command and kernels).
 TRAFFIC_BYTES = {
-    "q4_0_ffn_decode_token": 19169075,
+    "q4_0_ffn_decode_token": 19188531,
     "q8_0_matvec_2048x2048": 4645683,
-    "q8_0_lm_head_262144x2048_argmax": 577968640,
+    "q8_0_lm_head_262144x2048_argmax": 572300800,
     "q4_k_batched_8192x2048_m1": 9658163,
-    "q4_k_batched_8192x2048_m8": 10421043,
-    "q4_k_batched_8192x2048_m64": 15926067,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40050483,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 593801728,
+    "q4_k_batched_8192x2048_m8": 10430259,
+    "q4_k_batched_8192x2048_m32": 16970547,
+    "q4_k_batched_8192x2048_m64": 32674611,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40063181,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 581835059,
+    "q5_k_matvec_8192x2048": 11767603,
+    "q6_k_matvec_8192x2048": 14026547,
+    "q4_0_ffn_block_decode_token": 29156147,
+    "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572358144,
+    "attention_decode_h16_kv8_d256_len8192": 139053978,
 }
 
 
@@ -72,6 +79,8 @@ class Workload:
     step_bytes = 0          # algorithmic bytes per step
     dominant_name = ""           # dominant kernel name (as rocprof reports it)
     dominant_bytes = 0      # algorithmic bytes per launch of the dominant kernel
+    bound = "hbm"           # roofline the dominant kernel is judged against ("hbm" or "mfma")
+    dominant_flops = 0      # useful flops per launch (bound "mfma")
     tokens_per_step = 0     # MoE: tokens per step
     copies = 1
 
@@ -172,7 +181,7 @@ class MatvecQ8_0(Workload):
 
 class LmHeadQ8_0(Workload):
     name = "q8_0_lm_head_262144x2048_argmax"
-    dominant_name = "k_rows<FmtQ8_0, 32, EPI_ARGMAX>"
+    dominant_name = "k_rows<FmtQ8_0, 32, EPI_ARGMAX> + k_argmax_final"
 
     def __init__(self, g4, ctx, torch):
         import synth
@@ -211,12 +220,14 @@ class LmHeadQ8_0(Workload):
 
 
 class BatchedQ4_K(Workload):
-    dominant_name = "k_rows<FmtQ4_K, 32, EPI_STORE> (M segments)"
-
     def __init__(self, g4, ctx, torch, m=8):
         import synth
         c = synth.q4_k_batched(m)
         self.c, self.m = c, m
+        # one token: the row-stream kernel; several: the matrix-core kernel (1, 2 or 4
+        # token tiles per wave) plus the column-split reduce when it splits columns
+        self.dominant_name = ("k_rows<FmtQ4_K, 32, EPI_STORE>" if m == 1 else
+                              "k_tok_q4k<TT> (+ k_tok_reduce), bf16x3 MFMA 16x16x32")
         self.name = "q4_k_batched_8192x2048_m%d" % m
         R, D = c["dim0"], c["dim1"]
         self.R, self.D = R, D
@@ -226,6 +237,10 @@ class BatchedQ4_K(Workload):
         self.Y = torch.empty((m, R), dtype=torch.float32, device="cuda")
         self.step_bytes = c["w"].nbytes + 4 * m * (D + R)
         self.dominant_bytes = self.step_bytes
+        self.dominant_flops = 2 * m * R * D
+        # arithmetic intensity 3.6 M flop/B: past the HBM ridge of the exact-fp32
+        # scheme (three bf16 products per weight) from M = 32 on
+        self.bound = "mfma" if m >= 32 else "hbm"
 
     def step(self, i):
         self.w[i % self.copies].matmul_batch_dev(self.X, self.m, self.Y, self.R, self.D)
@@ -624,6 +639,17 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool)
         value = wl.step_bytes / (ms_per_step / 1e3) / 1e9
         gbs_step = value
     achieved = wl.dominant_bytes / (kern_ms / 1e3) / 1e9
+    if wl.bound == "mfma":
+        tflops = wl.dominant_flops / (kern_ms / 1e3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(tflops, 3), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5), "traffic": TRAFFIC_BYTES.get(wl.name),
+                    "hbm_gbs": round(achieved, 2), "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "note": "useful flops 2*M*rows*cols; each fp32 product is three exact bf16 MFMA products"}
+    else:
+        roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES.get(wl.name)}
+    roofline.update({"kernel": wl.dominant_name, "bytes_per_launch": wl.dominant_bytes,
+                     "avg_launch_us": round(kern_ms * 1e3, 3), "launches_timed": launches})
     line = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -639,10 +665,7 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool)
         "data": "synthetic: seeded GGUF blocks and activations (gemma4.kt_amd/synth.py)",
         "config": dict(wl.config(), graph=step_graph is not None, step_gbs=round(gbs_step, 2),
                        hbm_fraction=round(gbs_step / HBM_PEAK_GBS, 4)),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES.get(wl.name),
-                     "kernel": wl.dominant_name, "bytes_per_launch": wl.dominant_bytes,
-                     "avg_launch_us": round(kern_ms * 1e3, 3), "launches_timed": launches},
+        "roofline": roofline,
     }
     if cpu_seconds > 0 and not isinstance(wl, CopyCalibration):
         line["cpu_baseline"] = cpu_baseline(wl, cpu_seconds)
