@@ -541,7 +541,8 @@ G4_DEV float wave_sum(float v) {
 // parallel reduction: larger value wins, equal values go to the lower index.
 // Callers map NaN to -inf (never wins) except at index 0, where it maps to +inf
 // (the sequential scan keeps a NaN first element).
-G4_DEV bool am_better(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
+// Bitwise, not short-circuit: `||`/`&&` here compiled to a branch per comparison.
+G4_DEV bool am_better(float a, int ia, float b, int ib) { return (a > b) | ((a == b) & (ia < ib)); }
 G4_DEV float am_key(float v, int64_t idx) { return v != v ? (idx == 0 ? __builtin_inff() : -__builtin_inff()) : v; }
 
 // Value of the butterfly partner at distance S (lane ^ S for S >= 16 and S = 8,

@@ -411,7 +411,7 @@ __global__ __launch_bounds__(256) void k_argmax(const float *v, int32_t n, float
 }
 
 // ------------------------------------------------------------------ route ----
-// One 64-lane block per token.  Softmax of MutableFloatTensor.kt:54-59 (max with
+// One 256-thread block per token.  Softmax of MutableFloatTensor.kt:54-59 (max with
 // java.lang.Math.max semantics, exp in double, fp32 sum in index order, fp32
 // divide), top-k of Llama.kt:275-293 (strict >, ties to the lowest index,
 // chosen entries masked to -inf), optional renormalisation (fp32 sum in k
@@ -425,51 +425,105 @@ G4_DEV float java_max(float a, float b) {
   return a >= b ? a : b;
 }
 
-__global__ __launch_bounds__(64) void k_route(const float *logits, int32_t E, int32_t K, int32_t renorm,
-                                              const float *expert_scale, int32_t *ids, float *weights) {
+__global__ __launch_bounds__(256) void k_route(const float *logits, int32_t E, int32_t K, int32_t renorm,
+                                               const float *expert_scale, int32_t *ids, float *weights) {
   __shared__ float p[ROUTE_MAX_E];
   __shared__ float pick_w[ROUTE_MAX_E];
   __shared__ int32_t pick_i[ROUTE_MAX_E];
   __shared__ float es[ROUTE_MAX_E];
-  const int t = blockIdx.x, lane = threadIdx.x;
+  __shared__ uint64_t key[ROUTE_MAX_E];
+  __shared__ float wm[4];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const float *lg = logits + (int64_t)t * E;
   // the expert scales come in with the logits (not in a dependent load at the end)
   if (expert_scale)
-    for (int i = lane; i < E; i += 64) es[i] = expert_scale[i];
+    for (int i = tid; i < E; i += 256) es[i] = expert_scale[i];
+  // max with Math.max semantics (order-independent: NaN wins, +0 over -0)
   float m = -__builtin_inff();
-  for (int i = lane; i < E; i += 64) m = java_max(m, lg[i]);
+  for (int i = tid; i < E; i += 256) m = java_max(m, lg[i]);
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) m = java_max(m, __shfl_xor(m, s, 64));
-  for (int i = lane; i < E; i += 64) p[i] = (float)exp((double)__fsub_rn(lg[i], m));
+  if (lane == 0) wm[wid] = m;
   __syncthreads();
-  // fp32 sum in index order: every lane adds the same sequence (LDS broadcast
-  // reads), so the sum needs no second barrier
+  m = java_max(java_max(wm[0], wm[1]), java_max(wm[2], wm[3]));
+  for (int i = tid; i < E; i += 256) p[i] = (float)exp((double)__fsub_rn(lg[i], m));
+  __syncthreads();
+  // fp32 sum in index order: every thread adds the same sequence (LDS broadcast
+  // reads), so the sum needs no second barrier.  32 reads go out before their adds.
   float sum = 0.f;
-  for (int i = 0; i < E; ++i) sum = __fadd_rn(sum, p[i]);
-  __syncthreads();
-  for (int i = lane; i < E; i += 64) p[i] = __fdiv_rn(p[i], sum);
-  __syncthreads();
-  // the picks stay in LDS; every lane keeps the same running renormalisation sum
-  float renorm_sum = 0.f;
-  for (int j = 0; j < K; ++j) {
-    float bv = -__builtin_inff();
-    int bi = INT_MAX;
-    for (int i = lane; i < E; i += 64) {
-      const float v = p[i] != p[i] ? -__builtin_inff() : p[i];
-      if (am_better(v, i, bv, bi)) bv = v, bi = i;
-    }
-    am_wave(bv, bi);
-    if (bv == -__builtin_inff()) bi = 0;  // no entry beats the initial -inf: the scan keeps index 0
-    renorm_sum = __fadd_rn(renorm_sum, bv);
-    __syncthreads();
-    if (lane == 0) {
-      pick_i[j] = bi;
-      pick_w[j] = bv;
-      p[bi] = -__builtin_inff();
-    }
-    __syncthreads();
+  int i0 = 0;
+  for (; i0 + 32 <= E; i0 += 32) {
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = p[i0 + j];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) sum = __fadd_rn(sum, v[j]);
   }
-  for (int j = lane; j < K; j += 64) {
+  for (; i0 < E; ++i0) sum = __fadd_rn(sum, p[i0]);
+  __syncthreads();
+  bool nan = false;
+  for (int i = tid; i < E; i += 256) {
+    const float q = __fdiv_rn(p[i], sum);
+    p[i] = q;
+    nan |= q != q;
+  }
+  // Top-k of Llama.kt:275-293 (K scans with strict >, the winner masked to -inf).
+  // Without NaN every probability is finite and >= 0, and those scans pick the
+  // elements in order of (larger value, then lower index): element i's rank is
+  // the number of elements that beat it, computed by every thread for its own
+  // elements at once.  With a NaN present the scans themselves run (a NaN never
+  // wins; once nothing beats -inf the scan keeps index 0).
+  if (!__syncthreads_or(nan)) {
+    // (value, index) as one 64-bit key: p >= 0 is finite here, so its bits order
+    // as an unsigned integer, and the low word ranks lower indices higher
+    for (int i = tid; i < E; i += 256) key[i] = ((uint64_t)__float_as_uint(p[i]) << 32) | (uint32_t)(~i);
+    __syncthreads();
+    // element i's rank = number of keys above key[i]; `parts` threads share one
+    // element's scan, four independent counters each
+    int parts = 1;  // a power of two <= 64 with parts * E <= 256
+    while (parts < 64 && 2 * parts * E <= 256) parts *= 2;
+    const int part = tid % parts;
+    for (int i = tid / parts; i < E; i += 256 / parts) {
+      const uint64_t ki = key[i];
+      int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+      const int j0 = part * E / parts, j1 = (part + 1) * E / parts;
+      int j = j0;
+      for (; j + 4 <= j1; j += 4) {
+        r0 += (int)(key[j] > ki);
+        r1 += (int)(key[j + 1] > ki);
+        r2 += (int)(key[j + 2] > ki);
+        r3 += (int)(key[j + 3] > ki);
+      }
+      for (; j < j1; ++j) r0 += (int)(key[j] > ki);
+      int r = (r0 + r1) + (r2 + r3);
+      // the parts of one element are adjacent lanes of one wave
+      for (int m = 1; m < parts; m <<= 1) r += __shfl_xor(r, m, 64);
+      if (part == 0 && r < K) pick_w[r] = p[i], pick_i[r] = i;
+    }
+  } else {
+    for (int j = 0; j < K; ++j) {
+      float bv = -__builtin_inff();
+      int bi = INT_MAX;
+      for (int i = tid; i < E; i += 256) {
+        const float v = p[i] != p[i] ? -__builtin_inff() : p[i];
+        if (am_better(v, i, bv, bi)) bv = v, bi = i;
+      }
+      am_block(bv, bi);  // thread 0 holds the winner
+      if (tid == 0) {
+        if (bv == -__builtin_inff()) bi = 0;
+        pick_i[j] = bi;
+        pick_w[j] = bv;
+        p[bi] = -__builtin_inff();
+      }
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  // renormalisation sum in k order, the same in every thread
+  float renorm_sum = 0.f;
+  if (renorm)
+    for (int j = 0; j < K; ++j) renorm_sum = __fadd_rn(renorm_sum, pick_w[j]);
+  for (int j = tid; j < K; j += 256) {
     const int id = pick_i[j];
     float w = pick_w[j];
     if (renorm) w = __fdiv_rn(w, renorm_sum);
@@ -486,8 +540,19 @@ __global__ void k_moe_combine(const float *ys, const float *w, int32_t T, int32_
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = i / dim, r = i % dim;
     float out = 0.f;
-    for (int j = 0; j < K; ++j)
-      out = __fadd_rn(__fmul_rn(w[t * K + j], ys[(t * K + j) * dim + r]), out);
+    // eight slots' loads go out before their ordered adds
+    for (int j0 = 0; j0 < K; j0 += 8) {
+      float a[8], v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u < K ? j0 + u : K - 1;
+        a[u] = w[t * K + j];
+        v[u] = ys[(t * K + j) * dim + r];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (j0 + u < K) out = __fadd_rn(__fmul_rn(a[u], v[u]), out);
+    }
     Y[i] = out;
   }
 }
@@ -780,7 +845,7 @@ hipError_t launch_argmax(const float *v, int32_t n, float *part_val, int32_t *pa
 hipError_t launch_route(const float *logits, int32_t T, int32_t n_experts, int32_t k, int32_t renorm,
                         const float *expert_scale, int32_t *ids, float *weights, hipStream_t s) {
   if (n_experts > ROUTE_MAX_E) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_route, dim3(T), dim3(64), 0, s, logits, n_experts, k, renorm, expert_scale, ids, weights);
+  hipLaunchKernelGGL(k_route, dim3(T), dim3(256), 0, s, logits, n_experts, k, renorm, expert_scale, ids, weights);
   return hipGetLastError();
 }
 

@@ -373,3 +373,36 @@ def test_argmax_cases(g4, ctx, oracle, case):
         v[1000] = -0.0
         v[2000] = 0.0
     assert g4.argmax(ctx, v) == oracle.argmax(v)
+
+
+@pytest.mark.parametrize("case", ["ties", "zeros", "nan", "e100", "e300", "e1024", "k_all"])
+def test_moe_route_edge_cases(g4, ctx, oracle, case):
+    """Top-k ties (lowest index first), probabilities that underflow to 0, a NaN
+    logit (the scans keep index 0 once nothing beats -inf), expert counts that are
+    not a multiple of the workgroup, and k = n_experts."""
+    announce("moe route %s" % case)
+    rng = np.random.default_rng(49)
+    E, K, T = 128, 8, 3
+    if case == "e100":
+        E = 100
+    elif case == "e300":
+        E = 300
+    elif case == "e1024":
+        E, K = 1024, 16
+    elif case == "k_all":
+        E, K = 64, 64
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    if case == "ties":
+        lg[:, :] = np.round(lg * 2) / 2      # many equal logits
+        lg[0, :] = 1.0                        # every logit equal
+    elif case == "zeros":
+        lg[:, :] = -1000.0                    # exp underflows to 0 except the maximum
+        lg[:, 5] = 0.0
+        lg[1, 70] = 0.0
+    elif case == "nan":
+        lg[1, 17] = np.nan
+    for renorm in (True, False):
+        ids, w = g4.moe_route(ctx, lg, K, renorm)
+        rids, rw = oracle.route(lg, K, renorm)
+        assert np.array_equal(ids, rids), (case, renorm)
+        assert same_bits(w, rw), (case, renorm)
