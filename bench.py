@@ -6,8 +6,10 @@ Default workload: the Q4_0 FFN of one decode token (gate/up W 8192x2048, down W
 y = W_down h -- two launches of libg4hip.so.  Weights are resident in HBM before
 timing starts; each step uses the next of several weight copies whose total
 exceeds twice the 256 MB Infinity Cache, so every step streams from HBM.
-Steps are captured in a HIP graph (one graph = one pass over the copies) and
-replayed; the timed region is bracketed by device synchronisation.
+Steps are captured in a HIP graph (one graph = whole passes over the copies,
+at least 8 steps, so a graph replay's own launch cost is spread over several
+steps as in a decode loop) and replayed; the timed region is bracketed by
+device synchronisation.
 
 Prints one JSON line.  `value` is GB/s of algorithmic bytes (each weight and
 activation byte counted once) per second; `roofline` covers the dominant
@@ -39,6 +41,7 @@ METRIC = "quant matvec GB/s & % of HBM peak (Q8_0/Q4_0/Q4_K); MoE expert tokens/
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 matrix-core peak
 MALL_BYTES = 256 << 20
+GRAPH_MIN_STEPS = 8  # steps per captured graph (whole passes over the copies)
 Q8_0, Q4_0, Q4_K = 8, 2, 12
 
 
@@ -260,7 +263,8 @@ class BatchedQ4_K(Workload):
 
 class MoeQ4_K(Workload):
     unit = "tokens/s"
-    dominant_name = "expert launches of g4_moe: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR> + k_rows<FmtQ4_K, 32> + k_moe_combine"
+    dominant_name = ("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE> (routing + gate_up) + "
+                     "k_rows<FmtQ4_K, 32> (down) + k_moe_combine")
 
     def __init__(self, g4, ctx, torch, tokens=1, routings=32):
         import synth
@@ -287,24 +291,18 @@ class MoeQ4_K(Workload):
         per_expert = (2 * FF * D + D * FF) // 256 * 144
         self.per_expert = per_expert
         mean_distinct = float(np.mean(self.distinct))
+        # a step reads every routed expert's gate_up and down once, x and the router
+        # logits, and writes Y (the routing outputs are 8 bytes per slot)
         self.step_bytes = int(mean_distinct * per_expert + 4 * tokens * (D + E + D))
-        # the timed group (g4_moe) reads every routed expert's gate_up and down once,
-        # x, and writes Y; the router logits belong to the separate route launch
-        self.dominant_bytes = int(mean_distinct * per_expert + 4 * tokens * (D + D))
+        self.dominant_bytes = self.step_bytes
         self.tokens_per_step = tokens
         self.g4, self.ctx = g4, ctx
 
     def step(self, i):
+        # routing (inside the gate_up launch), experts and the weighted sum
         r = i % self.copies
-        self.g4.moe_route_dev(self.ctx, self.logits[r], self.T, self.E, self.K, True, self.ids.data_ptr(), self.gw)
-        self.g4.moe_dev(self.ctx, self.wgu, self.wdn, self.X[r], self.T, self.D, self.FF, self.ids.data_ptr(),
-                        self.gw, self.K, self.Y)
-
-    def dominant(self, i):
-        # expert FFN launches of one routing (routing ids from the previous step's route)
-        r = i % self.copies
-        self.g4.moe_dev(self.ctx, self.wgu, self.wdn, self.X[r], self.T, self.D, self.FF, self.ids.data_ptr(),
-                        self.gw, self.K, self.Y)
+        self.g4.moe_routed_dev(self.ctx, self.wgu, self.wdn, self.X[r], self.T, self.D, self.FF, self.logits[r],
+                               self.E, self.K, True, self.ids.data_ptr(), self.gw, self.Y)
 
     def cpu_setup(self, oracle):
         self.oracle = oracle
@@ -576,7 +574,8 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool)
     ctx = g4.Context(0)
     wl = make_workload(spec, g4, ctx, torch)
     stream = torch.cuda.Stream()
-    copies = wl.copies
+    # one graph replays whole passes over the weight copies, at least GRAPH_MIN_STEPS steps
+    copies = wl.copies * max(1, math.ceil(GRAPH_MIN_STEPS / wl.copies))
     rounds = max(1, math.ceil(steps / copies))
     steps = rounds * copies
     dom_rounds = max(1, math.ceil(64 / copies))

@@ -304,9 +304,18 @@ int check_moe(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t T
   return G4_OK;
 }
 
+// Routing done inside the gate+up launch (g4_moe_routed*): the router logits in,
+// the ids and weights it stores out.
+struct MoeRoute {
+  const float *d_logits;
+  int32_t n_experts;
+  int32_t renormalize;
+  const float *d_scale;
+};
+
 int moe_dev(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t n_experts, const float *d_X, int32_t T,
             int32_t dim, int32_t ff, const int32_t *d_ids, const float *d_w, int32_t k, float *d_Y, float *d_h,
-            float *d_ys, float *d_gu) {
+            float *d_ys, float *d_gu, const MoeRoute *route = nullptr) {
   const int32_t S = T * k;  // (token, slot) pairs
   if (S == 0) {
     if (T > 0) G4_HIP(hipMemsetAsync(d_Y, 0, sizeof(float) * (size_t)T * dim, ctx->stream), "hipMemsetAsync");
@@ -314,12 +323,21 @@ int moe_dev(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t n_e
   }
   g4::RowsArgs a;
   memset(&a, 0, sizeof(a));
+  if (route) {
+    // d_ids / d_w are the outputs of the routing then
+    a.route_logits = route->d_logits;
+    a.route_scale = route->d_scale;
+    a.route_e = route->n_experts;
+    a.route_renorm = route->renormalize;
+    a.route_ids = const_cast<int32_t *>(d_ids);
+    a.route_w = const_cast<float *>(d_w);
+  }
   a.W0 = a.W1 = wgu->d;
   a.base0 = 0;
   a.base1 = (int64_t)ff * dim;
   a.row_stride = dim;
   a.expert_stride = 2 * (int64_t)ff * dim;
-  a.ids = d_ids;
+  a.ids = route ? nullptr : d_ids;
   a.expert_count = n_experts;
   a.rows = ff;
   a.dim1 = dim;
@@ -978,6 +996,72 @@ int g4_moe_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down,
   char *s = ctx->scratch;
   return moe_dev(ctx, w_gate_up, w_down, ne, d_X, T, dim, ff, d_ids, d_weights, k, d_Y, (float *)(s + oh),
                  (float *)(s + oys), (float *)(s + ogu));
+}
+
+static int check_moe_routed(int32_t n_experts_weights, int32_t n_experts, int32_t k) {
+  if (n_experts <= 0 || n_experts > 1024)
+    return fail(G4_ERR_INVALID_ARGUMENT, "n_experts %d outside 1..1024", n_experts);
+  if (n_experts > n_experts_weights)
+    return fail(G4_ERR_OUT_OF_RANGE, "%d router logits per token, the weights hold %d experts", n_experts,
+                n_experts_weights);
+  if (k < 0 || k > n_experts) return fail(G4_ERR_INVALID_ARGUMENT, "k %d outside 0..n_experts", k);
+  return G4_OK;
+}
+
+int g4_moe_routed(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *X, int32_t T,
+                  int32_t dim, int32_t ff, const float *logits, int32_t n_experts, int32_t k, int32_t renormalize,
+                  const float *expert_scale, int32_t *ids, float *weights, float *Y) {
+  G4_TRY(check_ctx(ctx));
+  int32_t ne = 0;
+  G4_TRY(check_moe(ctx, w_gate_up, w_down, T, dim, ff, k, &ne));
+  G4_TRY(check_moe_routed(ne, n_experts, k));
+  if (T == 0) return ok();
+  if (!X || !Y || !logits || (k > 0 && (!ids || !weights)))
+    return fail(G4_ERR_INVALID_ARGUMENT, "X/Y/logits/ids/weights is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t ox = c.add(sizeof(float) * (size_t)T * dim), ol = c.add(sizeof(float) * (size_t)T * n_experts),
+         os = c.add(sizeof(float) * (size_t)n_experts), oi = c.add(sizeof(int32_t) * (size_t)T * k),
+         ow = c.add(sizeof(float) * (size_t)T * k), oy = c.add(sizeof(float) * (size_t)T * dim);
+  size_t oh, oys, ogu;
+  moe_scratch(T, dim, ff, k, c, &oh, &oys, &ogu);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  char *s = ctx->scratch;
+  G4_TRY(copy_in(ctx, s + ox, X, sizeof(float) * (size_t)T * dim));
+  G4_TRY(copy_in(ctx, s + ol, logits, sizeof(float) * (size_t)T * n_experts));
+  if (expert_scale) G4_TRY(copy_in(ctx, s + os, expert_scale, sizeof(float) * (size_t)n_experts));
+  const MoeRoute route = {(const float *)(s + ol), n_experts, renormalize, expert_scale ? (const float *)(s + os) : nullptr};
+  G4_TRY(moe_dev(ctx, w_gate_up, w_down, ne, (const float *)(s + ox), T, dim, ff, (const int32_t *)(s + oi),
+                 (const float *)(s + ow), k, (float *)(s + oy), (float *)(s + oh), (float *)(s + oys),
+                 (float *)(s + ogu), &route));
+  G4_TRY(copy_out(ctx, Y, s + oy, sizeof(float) * (size_t)T * dim));
+  if (k > 0) {
+    G4_TRY(copy_out(ctx, ids, s + oi, sizeof(int32_t) * (size_t)T * k));
+    G4_TRY(copy_out(ctx, weights, s + ow, sizeof(float) * (size_t)T * k));
+  }
+  return finish(ctx);
+}
+
+int g4_moe_routed_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *d_X, int32_t T,
+                      int32_t dim, int32_t ff, const float *d_logits, int32_t n_experts, int32_t k,
+                      int32_t renormalize, const float *d_expert_scale, int32_t *d_ids, float *d_weights,
+                      float *d_Y) {
+  G4_TRY(check_ctx(ctx));
+  int32_t ne = 0;
+  G4_TRY(check_moe(ctx, w_gate_up, w_down, T, dim, ff, k, &ne));
+  G4_TRY(check_moe_routed(ne, n_experts, k));
+  if (T == 0) return ok();
+  if (!d_X || !d_Y || !d_logits || (k > 0 && (!d_ids || !d_weights)))
+    return fail(G4_ERR_INVALID_ARGUMENT, "X/Y/logits/ids/weights is null");
+  G4_TRY(use_device(ctx));
+  Carve c;
+  size_t oh, oys, ogu;
+  moe_scratch(T, dim, ff, k, c, &oh, &oys, &ogu);
+  G4_TRY(ensure_scratch(ctx, c.off));
+  char *s = ctx->scratch;
+  const MoeRoute route = {d_logits, n_experts, renormalize, d_expert_scale};
+  return moe_dev(ctx, w_gate_up, w_down, ne, d_X, T, dim, ff, d_ids, d_weights, k, d_Y, (float *)(s + oh),
+                 (float *)(s + oys), (float *)(s + ogu), &route);
 }
 
 // ---------------------------------------------------------- decode step ----

@@ -43,6 +43,18 @@ struct RowsArgs {
   const float *norm_w;
   float norm_eps;
   float *norm_out;
+  // MoE routing in the gate+up launch (EPI_GELU_PAIR) when route_logits != null:
+  // segment s is (token s / x_div, slot s % x_div), k = x_div.  Every workgroup
+  // routes its token from route_logits[token * route_e ...] (Llama.kt:269-293)
+  // and takes its slot's expert; the workgroups with blockIdx.x == 0 store the
+  // slot's expert id and weight to route_ids / route_w for the later launches.
+  // ids is unused then.
+  const float *route_logits;
+  const float *route_scale;
+  int32_t route_e;
+  int32_t route_renorm;
+  int32_t *route_ids;
+  float *route_w;
 };
 
 // Device facts used for launch sizing.

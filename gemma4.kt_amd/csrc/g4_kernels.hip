@@ -79,9 +79,139 @@ __global__ __launch_bounds__(256) void k_argmax_final(const float *pv, const int
   if (threadIdx.x == 0) *out = i;
 }
 
+// ------------------------------------------------------------------ route ----
+// Routing of one token by one 256-thread block: softmax of MutableFloatTensor.kt:54-59
+// (max with java.lang.Math.max semantics, exp in double, fp32 sum in index order,
+// fp32 divide), top-k of Llama.kt:275-293 (strict >, ties to the lowest index,
+// chosen entries masked to -inf), optional renormalisation (fp32 sum in k
+// order) and expert scale.  Used by k_route and by the routed gate+up launch.
+constexpr int ROUTE_MAX_E = 1024;       // k_route
+constexpr int ROUTE_FUSED_MAX_E = 256;  // routing inside the gate+up launch
+
+G4_DEV float java_max(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  if (a == 0.f && b == 0.f) return __builtin_signbit(a) ? b : a;
+  return a >= b ? a : b;
+}
+
+template <int MAXE>
+struct RouteLds {
+  float p[MAXE];
+  float es[MAXE];
+  uint64_t key[MAXE];
+  float pick_w[MAXE];
+  int32_t pick_i[MAXE];
+  float w_out[MAXE];
+  float wm[4];
+};
+
+// Leaves pick k's expert in r.pick_i[k] and its final weight in r.w_out[k],
+// visible to every thread of the block on return (E <= MAXE, K <= E; every
+// thread calls, uniform control flow).
+template <int MAXE>
+G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *expert_scale, RouteLds<MAXE> &r) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  // the expert scales come in with the logits (not in a dependent load at the end)
+  if (expert_scale)
+    for (int i = tid; i < E; i += 256) r.es[i] = expert_scale[i];
+  // max with Math.max semantics (order-independent: NaN wins, +0 over -0)
+  float m = -__builtin_inff();
+  for (int i = tid; i < E; i += 256) m = java_max(m, lg[i]);
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) m = java_max(m, __shfl_xor(m, s, 64));
+  if (lane == 0) r.wm[wid] = m;
+  __syncthreads();
+  m = java_max(java_max(r.wm[0], r.wm[1]), java_max(r.wm[2], r.wm[3]));
+  for (int i = tid; i < E; i += 256) r.p[i] = (float)exp((double)__fsub_rn(lg[i], m));
+  __syncthreads();
+  // fp32 sum in index order: every thread adds the same sequence (LDS broadcast
+  // reads), so the sum needs no second barrier.  32 reads go out before their adds.
+  float sum = 0.f;
+  int i0 = 0;
+  for (; i0 + 32 <= E; i0 += 32) {
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = r.p[i0 + j];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) sum = __fadd_rn(sum, v[j]);
+  }
+  for (; i0 < E; ++i0) sum = __fadd_rn(sum, r.p[i0]);
+  __syncthreads();
+  bool nan = false;
+  for (int i = tid; i < E; i += 256) {
+    const float q = __fdiv_rn(r.p[i], sum);
+    r.p[i] = q;
+    nan |= q != q;
+  }
+  // Top-k of Llama.kt:275-293 (K scans with strict >, the winner masked to -inf).
+  // Without NaN every probability is finite and >= 0, and those scans pick the
+  // elements in order of (larger value, then lower index): element i's rank is
+  // the number of elements that beat it, computed by every thread for its own
+  // elements at once.  With a NaN present the scans themselves run (a NaN never
+  // wins; once nothing beats -inf the scan keeps index 0).
+  if (!__syncthreads_or(nan)) {
+    // (value, index) as one 64-bit key: p >= 0 is finite here, so its bits order
+    // as an unsigned integer, and the low word ranks lower indices higher
+    for (int i = tid; i < E; i += 256) r.key[i] = ((uint64_t)__float_as_uint(r.p[i]) << 32) | (uint32_t)(~i);
+    __syncthreads();
+    // element i's rank = number of keys above key[i]; `parts` threads share one
+    // element's scan, four independent counters each
+    int parts = 1;  // a power of two <= 64 with parts * E <= 256
+    while (parts < 64 && 2 * parts * E <= 256) parts *= 2;
+    const int part = tid % parts;
+    for (int i = tid / parts; i < E; i += 256 / parts) {
+      const uint64_t ki = r.key[i];
+      int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+      const int j0 = part * E / parts, j1 = (part + 1) * E / parts;
+      int j = j0;
+      for (; j + 4 <= j1; j += 4) {
+        r0 += (int)(r.key[j] > ki);
+        r1 += (int)(r.key[j + 1] > ki);
+        r2 += (int)(r.key[j + 2] > ki);
+        r3 += (int)(r.key[j + 3] > ki);
+      }
+      for (; j < j1; ++j) r0 += (int)(r.key[j] > ki);
+      int rank = (r0 + r1) + (r2 + r3);
+      // the parts of one element are adjacent lanes of one wave
+      for (int o = 1; o < parts; o <<= 1) rank += __shfl_xor(rank, o, 64);
+      if (part == 0 && rank < K) r.pick_w[rank] = r.p[i], r.pick_i[rank] = i;
+    }
+  } else {
+    for (int j = 0; j < K; ++j) {
+      float bv = -__builtin_inff();
+      int bi = INT_MAX;
+      for (int i = tid; i < E; i += 256) {
+        const float v = r.p[i] != r.p[i] ? -__builtin_inff() : r.p[i];
+        if (am_better(v, i, bv, bi)) bv = v, bi = i;
+      }
+      am_block(bv, bi);  // thread 0 holds the winner
+      if (tid == 0) {
+        if (bv == -__builtin_inff()) bi = 0;
+        r.pick_i[j] = bi;
+        r.pick_w[j] = bv;
+        r.p[bi] = -__builtin_inff();
+      }
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  // renormalisation sum in k order, the same in every thread
+  float renorm_sum = 0.f;
+  if (renorm)
+    for (int j = 0; j < K; ++j) renorm_sum = __fadd_rn(renorm_sum, r.pick_w[j]);
+  for (int j = tid; j < K; j += 256) {
+    float w = r.pick_w[j];
+    if (renorm) w = __fdiv_rn(w, renorm_sum);
+    if (expert_scale) w = __fmul_rn(w, r.es[r.pick_i[j]]);
+    r.w_out[j] = w;
+  }
+  __syncthreads();
+}
+
 // --------------------------------------------------------------- engine ----
 
-template <class F, int LPR, int CPL, int EPI, bool MULTI, bool NORM>
+template <class F, int LPR, int CPL, int EPI, bool MULTI, bool NORM, bool ROUTE = false>
 __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1;  // row steps per tile (about F::RT chunk loads per lane)
   constexpr int RPW = 64 / LPR;                  // rows in flight per step (one per lane group)
@@ -94,6 +224,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   static_assert(EPI != EPI_GELU_PAIR || (RT >= 2 && CPL == 1), "paired tiles: gate and up steps, one pass");
   static_assert(XSEG >= 1 && XSEG * 256 == NCH * 16, "x staging");
   static_assert(!(NORM && MULTI), "the fused norm needs all of x in one pass");
+  static_assert(!ROUTE || (EPI == EPI_GELU_PAIR && !MULTI && !NORM), "routing: gate+up launches");
   __shared__ u32x4 xl[NCH * 16];
   __shared__ float red[4];
 
@@ -102,8 +233,19 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   constexpr int wpb = 4;                         // launched with 256 threads
   const int gi = lane / LPR, q = lane % LPR;
   const int seg = blockIdx.y;
-  const int expert = a.ids ? a.ids[seg] : 0;
-  const bool bad_expert = a.ids && (expert < 0 || expert >= a.expert_count);
+  int expert = 0;
+  if constexpr (ROUTE) {
+    // the token's routing, computed by every workgroup of its segments (the
+    // logits are 4 bytes per expert; a separate launch would cost more)
+    __shared__ RouteLds<ROUTE_FUSED_MAX_E> rl;
+    const int tok = seg / a.x_div, slot = seg % a.x_div;
+    route_token(a.route_logits + (int64_t)tok * a.route_e, a.route_e, a.x_div, a.route_renorm, a.route_scale, rl);
+    expert = __builtin_amdgcn_readfirstlane(rl.pick_i[slot]);
+    if (blockIdx.x == 0 && tid == 0) a.route_ids[seg] = expert, a.route_w[seg] = rl.w_out[slot];
+  } else if (a.ids) {
+    expert = a.ids[seg];
+  }
+  const bool bad_expert = (ROUTE || a.ids) && (expert < 0 || expert >= a.expert_count);
   const int64_t ebase = bad_expert ? 0 : (int64_t)expert * a.expert_stride;
   const float *x = a.x + (int64_t)(seg / a.x_div) * a.x_stride;
   float *y = a.y ? a.y + (int64_t)seg * a.y_stride : nullptr;
@@ -411,125 +553,15 @@ __global__ __launch_bounds__(256) void k_argmax(const float *v, int32_t n, float
 }
 
 // ------------------------------------------------------------------ route ----
-// One 256-thread block per token.  Softmax of MutableFloatTensor.kt:54-59 (max with
-// java.lang.Math.max semantics, exp in double, fp32 sum in index order, fp32
-// divide), top-k of Llama.kt:275-293 (strict >, ties to the lowest index,
-// chosen entries masked to -inf), optional renormalisation (fp32 sum in k
-// order) and expert scale.
-constexpr int ROUTE_MAX_E = 1024;
-
-G4_DEV float java_max(float a, float b) {
-  if (a != a) return a;
-  if (b != b) return b;
-  if (a == 0.f && b == 0.f) return __builtin_signbit(a) ? b : a;
-  return a >= b ? a : b;
-}
-
+// One 256-thread block per token (route_token).
 __global__ __launch_bounds__(256) void k_route(const float *logits, int32_t E, int32_t K, int32_t renorm,
                                                const float *expert_scale, int32_t *ids, float *weights) {
-  __shared__ float p[ROUTE_MAX_E];
-  __shared__ float pick_w[ROUTE_MAX_E];
-  __shared__ int32_t pick_i[ROUTE_MAX_E];
-  __shared__ float es[ROUTE_MAX_E];
-  __shared__ uint64_t key[ROUTE_MAX_E];
-  __shared__ float wm[4];
-  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const float *lg = logits + (int64_t)t * E;
-  // the expert scales come in with the logits (not in a dependent load at the end)
-  if (expert_scale)
-    for (int i = tid; i < E; i += 256) es[i] = expert_scale[i];
-  // max with Math.max semantics (order-independent: NaN wins, +0 over -0)
-  float m = -__builtin_inff();
-  for (int i = tid; i < E; i += 256) m = java_max(m, lg[i]);
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) m = java_max(m, __shfl_xor(m, s, 64));
-  if (lane == 0) wm[wid] = m;
-  __syncthreads();
-  m = java_max(java_max(wm[0], wm[1]), java_max(wm[2], wm[3]));
-  for (int i = tid; i < E; i += 256) p[i] = (float)exp((double)__fsub_rn(lg[i], m));
-  __syncthreads();
-  // fp32 sum in index order: every thread adds the same sequence (LDS broadcast
-  // reads), so the sum needs no second barrier.  32 reads go out before their adds.
-  float sum = 0.f;
-  int i0 = 0;
-  for (; i0 + 32 <= E; i0 += 32) {
-    float v[32];
-#pragma unroll
-    for (int j = 0; j < 32; ++j) v[j] = p[i0 + j];
-#pragma unroll
-    for (int j = 0; j < 32; ++j) sum = __fadd_rn(sum, v[j]);
-  }
-  for (; i0 < E; ++i0) sum = __fadd_rn(sum, p[i0]);
-  __syncthreads();
-  bool nan = false;
-  for (int i = tid; i < E; i += 256) {
-    const float q = __fdiv_rn(p[i], sum);
-    p[i] = q;
-    nan |= q != q;
-  }
-  // Top-k of Llama.kt:275-293 (K scans with strict >, the winner masked to -inf).
-  // Without NaN every probability is finite and >= 0, and those scans pick the
-  // elements in order of (larger value, then lower index): element i's rank is
-  // the number of elements that beat it, computed by every thread for its own
-  // elements at once.  With a NaN present the scans themselves run (a NaN never
-  // wins; once nothing beats -inf the scan keeps index 0).
-  if (!__syncthreads_or(nan)) {
-    // (value, index) as one 64-bit key: p >= 0 is finite here, so its bits order
-    // as an unsigned integer, and the low word ranks lower indices higher
-    for (int i = tid; i < E; i += 256) key[i] = ((uint64_t)__float_as_uint(p[i]) << 32) | (uint32_t)(~i);
-    __syncthreads();
-    // element i's rank = number of keys above key[i]; `parts` threads share one
-    // element's scan, four independent counters each
-    int parts = 1;  // a power of two <= 64 with parts * E <= 256
-    while (parts < 64 && 2 * parts * E <= 256) parts *= 2;
-    const int part = tid % parts;
-    for (int i = tid / parts; i < E; i += 256 / parts) {
-      const uint64_t ki = key[i];
-      int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
-      const int j0 = part * E / parts, j1 = (part + 1) * E / parts;
-      int j = j0;
-      for (; j + 4 <= j1; j += 4) {
-        r0 += (int)(key[j] > ki);
-        r1 += (int)(key[j + 1] > ki);
-        r2 += (int)(key[j + 2] > ki);
-        r3 += (int)(key[j + 3] > ki);
-      }
-      for (; j < j1; ++j) r0 += (int)(key[j] > ki);
-      int r = (r0 + r1) + (r2 + r3);
-      // the parts of one element are adjacent lanes of one wave
-      for (int m = 1; m < parts; m <<= 1) r += __shfl_xor(r, m, 64);
-      if (part == 0 && r < K) pick_w[r] = p[i], pick_i[r] = i;
-    }
-  } else {
-    for (int j = 0; j < K; ++j) {
-      float bv = -__builtin_inff();
-      int bi = INT_MAX;
-      for (int i = tid; i < E; i += 256) {
-        const float v = p[i] != p[i] ? -__builtin_inff() : p[i];
-        if (am_better(v, i, bv, bi)) bv = v, bi = i;
-      }
-      am_block(bv, bi);  // thread 0 holds the winner
-      if (tid == 0) {
-        if (bv == -__builtin_inff()) bi = 0;
-        pick_i[j] = bi;
-        pick_w[j] = bv;
-        p[bi] = -__builtin_inff();
-      }
-      __syncthreads();
-    }
-  }
-  __syncthreads();
-  // renormalisation sum in k order, the same in every thread
-  float renorm_sum = 0.f;
-  if (renorm)
-    for (int j = 0; j < K; ++j) renorm_sum = __fadd_rn(renorm_sum, pick_w[j]);
-  for (int j = tid; j < K; j += 256) {
-    const int id = pick_i[j];
-    float w = pick_w[j];
-    if (renorm) w = __fdiv_rn(w, renorm_sum);
-    if (expert_scale) w = __fmul_rn(w, es[id]);
-    ids[(int64_t)t * K + j] = id;
-    weights[(int64_t)t * K + j] = w;
+  __shared__ RouteLds<ROUTE_MAX_E> r;
+  const int t = blockIdx.x;
+  route_token(logits + (int64_t)t * E, E, K, renorm, expert_scale, r);
+  for (int j = threadIdx.x; j < K; j += 256) {
+    ids[(int64_t)t * K + j] = r.pick_i[j];
+    weights[(int64_t)t * K + j] = r.w_out[j];
   }
 }
 
@@ -680,7 +712,9 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
   typedef void (*Kernel)(RowsArgs);
   const bool multi = (a.dim1 / 64) > LPR * CPL;
   const bool norm = a.norm_w != nullptr;
+  const bool route = a.route_logits != nullptr;
   if (norm && (multi || segments != 1)) return hipErrorInvalidValue;
+  if (route && (epi != EPI_GELU_PAIR || multi)) return hipErrorInvalidValue;
   Kernel k = nullptr;
   if (epi == EPI_STORE) {
     k = norm ? k_rows<F, LPR, CPL, EPI_STORE, false, true> : k_rows<F, LPR, CPL, EPI_STORE, false, false>;
@@ -691,16 +725,18 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
     if constexpr (LPR == 64 && CPL == 2)
       if (multi) k = k_rows<F, LPR, CPL, EPI_ARGMAX, true, false>;
   } else {
-    if constexpr (CPL == 1 && F::RT >= 2)
-      k = norm ? k_rows<F, LPR, 1, EPI_GELU_PAIR, false, true> : k_rows<F, LPR, 1, EPI_GELU_PAIR, false, false>;
+    if constexpr (CPL == 1 && F::RT >= 2) {
+      if (route) k = norm ? nullptr : k_rows<F, LPR, 1, EPI_GELU_PAIR, false, false, true>;
+      else k = norm ? k_rows<F, LPR, 1, EPI_GELU_PAIR, false, true> : k_rows<F, LPR, 1, EPI_GELU_PAIR, false, false>;
+    }
   }
   if (!k) return hipErrorInvalidValue;
   if (multi && !(LPR == 64 && CPL == 2)) return hipErrorInvalidValue;
 
   // Resident 256-thread workgroups per CU for this kernel (register-limited);
   // the launch fills exactly that many waves when there are tiles enough.
-  static int resident[3][2][2];
-  int &res = resident[epi][multi ? 1 : 0][norm ? 1 : 0];
+  static int resident[3][2][2][2];
+  int &res = resident[epi][multi ? 1 : 0][norm ? 1 : 0][route ? 1 : 0];
   if (res == 0) {
     int nb = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 256, 0) != hipSuccess || nb < 1) nb = 2;
@@ -773,6 +809,19 @@ static hipError_t launch_generic(int type, const RowsArgs &a, int nmat, int segm
 
 hipError_t launch_rows(int type, int epi, const RowsArgs &a, int segments, const DevInfo &dev, float *scratch,
                        hipStream_t s) {
+  if (a.route_logits) {
+    if (epi != EPI_GELU_PAIR || a.norm_w || a.x_div <= 0 || segments % a.x_div != 0) return hipErrorInvalidValue;
+    if (!rows_fast_ok(type, a, true) || a.route_e > ROUTE_FUSED_MAX_E) {
+      // routing in its own launch; the expert rows then read the ids it stores
+      hipError_t e = launch_route(a.route_logits, segments / a.x_div, a.route_e, a.x_div, a.route_renorm,
+                                  a.route_scale, a.route_ids, a.route_w, s);
+      if (e != hipSuccess) return e;
+      RowsArgs b = a;
+      b.route_logits = nullptr;
+      b.ids = a.route_ids;
+      return launch_rows(type, epi, b, segments, dev, scratch, s);
+    }
+  }
   if (rows_fast_ok(type, a, epi == EPI_GELU_PAIR)) {
     switch (type) {
       case T_Q8_0: return launch_fast<FmtQ8_0>(epi, a, segments, dev, s);

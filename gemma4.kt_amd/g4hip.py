@@ -107,6 +107,8 @@ SIGNATURES = {
     "g4_moe_route_dev": [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp],
     "g4_moe": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp],
     "g4_moe_dev": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp],
+    "g4_moe_routed": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp],
+    "g4_moe_routed_dev": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp],
     "g4_rmsnorm_dev": [_vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, ctypes.c_int],
     "g4_rmsnorm_add_dev": [_vp, _vp, _vp, _vp, _i32, ctypes.c_float],
     "g4_add_dev": [_vp, _vp, _vp, _i32],
@@ -467,6 +469,34 @@ def moe_dev(ctx: Context, gate_up, down, X, T: int, dim: int, ff: int, ids, weig
     check(lib().g4_moe_dev(ctx.handle, gate_up.handle, down.handle, _ptr(_dev_f32(X, "X")), int(T), int(dim),
                            int(ff), _ptr(ids), _ptr(_dev_f32(weights, "weights")), int(k),
                            _ptr(_dev_f32(Y, "Y"))))
+
+
+def moe_routed(ctx: Context, gate_up: GpuFloatTensor, down: GpuFloatTensor, X: np.ndarray, logits: np.ndarray,
+               k: int, renormalize: bool, dim: int, ff: int, expert_scale: Optional[np.ndarray] = None):
+    """The MoE block of Llama.kt:269-337 from router logits [T x n_experts]:
+    routing, expert FFN and weighted sum in one call.  Returns (Y, ids, weights)."""
+    X = _f32(np.ascontiguousarray(X, dtype=np.float32), "X")
+    logits = _f32(np.ascontiguousarray(logits, dtype=np.float32), "logits")
+    T, E = logits.shape
+    if X.size != T * dim:
+        raise ValueError("X holds %d floats, %d tokens x dim %d need %d" % (X.size, T, dim, T * dim))
+    if expert_scale is not None:
+        expert_scale = _f32(np.ascontiguousarray(expert_scale, dtype=np.float32), "expert_scale")
+    ids = np.zeros((T, k), dtype=np.int32)
+    w = np.zeros((T, k), dtype=np.float32)
+    Y = np.empty((T, dim), dtype=np.float32)
+    check(lib().g4_moe_routed(ctx.handle, gate_up.handle, down.handle, _ptr(X), int(T), int(dim), int(ff),
+                              _ptr(logits), int(E), int(k), int(bool(renormalize)), _ptr(expert_scale), _ptr(ids),
+                              _ptr(w), _ptr(Y)))
+    return Y, ids, w
+
+
+def moe_routed_dev(ctx: Context, gate_up, down, X, T: int, dim: int, ff: int, logits, n_experts: int, k: int,
+                   renormalize: bool, ids, weights, Y, expert_scale=None) -> None:
+    check(lib().g4_moe_routed_dev(ctx.handle, gate_up.handle, down.handle, _ptr(_dev_f32(X, "X")), int(T),
+                                  int(dim), int(ff), _ptr(_dev_f32(logits, "logits")), int(n_experts), int(k),
+                                  int(bool(renormalize)), _ptr(_dev_f32(expert_scale, "expert_scale")), _ptr(ids),
+                                  _ptr(_dev_f32(weights, "weights")), _ptr(_dev_f32(Y, "Y"))))
 
 
 # ------------------------------------------------------------ decode step ---

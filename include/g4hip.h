@@ -159,6 +159,21 @@ int g4_moe(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, con
 int g4_moe_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *d_X, int32_t T,
                int32_t dim, int32_t ff, const int32_t *d_ids, const float *d_weights, int32_t k, float *d_Y);
 
+/* The routed MoE block of Llama.kt:269-337 from the router logits, in one call:
+ * the routing of g4_moe_route (softmax, top-k, renormalize, expert_scale) and the
+ * expert FFN and weighted sum of g4_moe.  logits [T x n_experts] (n_experts at
+ * most the experts the weights hold); the routing is also returned in ids and
+ * weights [T x k].  Up to 256 experts the routing runs inside the gate+up launch
+ * (each workgroup routes its own token); above that in a launch of its own.
+ * Results are identical to g4_moe_route followed by g4_moe. */
+int g4_moe_routed(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *X, int32_t T,
+                  int32_t dim, int32_t ff, const float *logits, int32_t n_experts, int32_t k, int32_t renormalize,
+                  const float *expert_scale, int32_t *ids, float *weights, float *Y);
+int g4_moe_routed_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *d_X, int32_t T,
+                      int32_t dim, int32_t ff, const float *d_logits, int32_t n_experts, int32_t k,
+                      int32_t renormalize, const float *d_expert_scale, int32_t *d_ids, float *d_weights,
+                      float *d_Y);
+
 /* ---- Decode step around the matvec: the activations stay in device memory. ----
  * Norm weights are uploaded F32 tensors (ModelLoader.kt:281-286 reads norms as
  * FloatBuffers and throws UnsupportedOperationException for any other type).

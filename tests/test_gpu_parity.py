@@ -312,6 +312,83 @@ def test_moe_q4_k(g4, ctx, oracle, tokens):
     Y = g4.moe(ctx, wgu, wdn, c["x"], ids, gw, D, FF)
     y64, bound = oracle.moe_exact(Q4_K, c["gate_up"], Q4_K, c["down"], c["x"], rids, rw, D, FF)
     assert_dots(Y.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe T=%d" % tokens)
+    # the routing inside the gate+up launch gives the same routing and output bits
+    Yr, idr, wr = g4.moe_routed(ctx, wgu, wdn, c["x"], c["logits"], K, True, D, FF)
+    assert np.array_equal(idr, rids) and same_bits(wr, rw)
+    assert same_bits(Yr, Y)
+
+
+@pytest.mark.parametrize("case", ["t1", "t5", "t16", "ref_gates", "nan", "ties", "e256", "e300", "generic",
+                                  "k_all"])
+def test_moe_routed(g4, ctx, oracle, case):
+    """g4_moe_routed: the routing runs inside the gate+up launch (up to 256 experts,
+    rows on the 64-element fast path) or in a launch of its own (more experts, or
+    the per-element path); either way the routing equals g4_moe_route's and the
+    oracle's exactly, and the output g4_moe's bit for bit."""
+    announce("moe routed %s" % case)
+    E, D, FF, K, T, renorm, fmt = 16, 512, 256, 4, 3, True, Q4_K
+    scale = None
+    if case in ("t1", "t5", "t16"):
+        T = int(case[1:])
+    elif case == "ref_gates":
+        renorm = False
+        scale = np.linspace(0.25, 2.0, E).astype(np.float32)
+    elif case == "e256":
+        E, D, FF, K = 256, 128, 64, 8
+    elif case == "e300":
+        E, D, FF, K = 300, 128, 64, 8
+    elif case == "generic":
+        D, FF = 96, 64      # gate+up rows of 96 elements: the per-element kernel
+    elif case == "k_all":
+        E, K = 8, 8
+    gu = synth.weights(54, "gu" + case, fmt, E * 2 * FF * D)
+    dn = synth.weights(54, "dn" + case, fmt, E * D * FF)
+    lg = synth.activations(54, "lg" + case, T * E).reshape(T, E)
+    X = synth.activations(54, "X" + case, T * D).reshape(T, D)
+    if case == "nan":
+        lg[1, 3] = np.nan
+    elif case == "ties":
+        lg[:, :] = np.round(lg * 2) / 2
+        lg[0, :] = 1.0
+    wgu = upload(g4, ctx, fmt, gu, E * 2 * FF * D)
+    wdn = upload(g4, ctx, fmt, dn, E * D * FF)
+    Yr, idr, wr = g4.moe_routed(ctx, wgu, wdn, X, lg, K, renorm, D, FF, scale)
+    rids, rw = oracle.route(lg, K, renorm, scale)
+    assert np.array_equal(idr, rids) and same_bits(wr, rw)
+    ids, gw = g4.moe_route(ctx, lg, K, renorm, scale)
+    Y = g4.moe(ctx, wgu, wdn, X, ids, gw, D, FF)
+    assert same_bits(Yr, Y)
+    y64, bound = oracle.moe_exact(fmt, gu, fmt, dn, X, rids, rw, D, FF)
+    assert_dots(Yr.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe routed %s" % case)
+
+
+def test_moe_routed_dev_calls(g4, ctx, oracle):
+    """The device entry point on resident buffers, twice in a row with fewer tokens
+    the second time: ids, weights and Y of each call match the host entry point."""
+    import torch
+    announce("moe routed dev calls")
+    E, D, FF, K = 32, 256, 128, 4
+    gu = synth.q4_k(55, "gu", E * 2 * FF * D)
+    dn = synth.q4_k(55, "dn", E * D * FF)
+    wgu = upload(g4, ctx, Q4_K, gu, E * 2 * FF * D)
+    wdn = upload(g4, ctx, Q4_K, dn, E * D * FF)
+    for call, T in enumerate([16, 3]):
+        lg = synth.activations(55, "lg%d" % call, T * E).reshape(T, E)
+        X = synth.activations(55, "X%d" % call, T * D).reshape(T, D)
+        Yh, idh, wh = g4.moe_routed(ctx, wgu, wdn, X, lg, K, True, D, FF)
+        d_ids = torch.full((T, K), -1, dtype=torch.int32, device="cuda")
+        d_w = torch.zeros((T, K), dtype=torch.float32, device="cuda")
+        d_Y = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        try:
+            g4.moe_routed_dev(ctx, wgu, wdn, torch.from_numpy(X).cuda(), T, D, FF, torch.from_numpy(lg).cuda(), E,
+                              K, True, d_ids.data_ptr(), d_w, d_Y)
+            torch.cuda.synchronize()
+        finally:
+            ctx.set_stream(None)
+        assert np.array_equal(d_ids.cpu().numpy(), idh), call
+        assert same_bits(d_w.cpu().numpy(), wh), call
+        assert same_bits(d_Y.cpu().numpy(), Yh), call
 
 
 def test_moe_repeated_calls(g4, ctx, oracle):
