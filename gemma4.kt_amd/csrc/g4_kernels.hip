@@ -87,6 +87,7 @@ __global__ __launch_bounds__(256) void k_argmax_final(const float *pv, const int
 // order) and expert scale.  Used by k_route and by the routed gate+up launch.
 constexpr int ROUTE_MAX_E = 1024;       // k_route
 constexpr int ROUTE_FUSED_MAX_E = 256;  // routing inside the gate+up launch
+constexpr int ROUTE_FILTER_MAX_K = 32;  // top-k through the candidate filter up to this k
 
 G4_DEV float java_max(float a, float b) {
   if (a != a) return a;
@@ -103,6 +104,8 @@ struct RouteLds {
   float pick_w[MAXE];
   int32_t pick_i[MAXE];
   float w_out[MAXE];
+  uint32_t gmax[ROUTE_FILTER_MAX_K];
+  int32_t n_cand;
   float wm[4];
 };
 
@@ -112,29 +115,55 @@ struct RouteLds {
 template <int MAXE>
 G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *expert_scale, RouteLds<MAXE> &r) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  // the expert scales come in with the logits (not in a dependent load at the end)
-  if (expert_scale)
-    for (int i = tid; i < E; i += 256) r.es[i] = expert_scale[i];
+  const bool filter = K >= 1 && K <= ROUTE_FILTER_MAX_K;
+  if (tid < ROUTE_FILTER_MAX_K) r.gmax[tid] = 0u;
+  if (tid == 0) r.n_cand = 0;
+  // thread tid's logits (and expert scales) in registers, all loads issued at
+  // once; lanes past E load element 0 and do not use it
+  constexpr int PER = (MAXE + 255) / 256;
+  float lv[PER], sv[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = tid + 256 * u;
+    lv[u] = lg[i < E ? i : 0];
+    sv[u] = expert_scale ? expert_scale[i < E ? i : 0] : 0.f;
+  }
   // max with Math.max semantics (order-independent: NaN wins, +0 over -0)
   float m = -__builtin_inff();
-  for (int i = tid; i < E; i += 256) m = java_max(m, lg[i]);
+#pragma unroll
+  for (int u = 0; u < PER; ++u)
+    if (tid + 256 * u < E) m = java_max(m, lv[u]);
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) m = java_max(m, __shfl_xor(m, s, 64));
   if (lane == 0) r.wm[wid] = m;
   __syncthreads();
   m = java_max(java_max(r.wm[0], r.wm[1]), java_max(r.wm[2], r.wm[3]));
-  for (int i = tid; i < E; i += 256) r.p[i] = (float)exp((double)__fsub_rn(lg[i], m));
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = tid + 256 * u;
+    if (i < E) {
+      r.p[i] = (float)exp((double)__fsub_rn(lv[u], m));
+      r.es[i] = sv[u];
+    }
+  }
   __syncthreads();
   // fp32 sum in index order: every thread adds the same sequence (LDS broadcast
-  // reads), so the sum needs no second barrier.  32 reads go out before their adds.
+  // reads), so the sum needs no second barrier.  64 reads go out before their adds.
   float sum = 0.f;
   int i0 = 0;
-  for (; i0 + 32 <= E; i0 += 32) {
-    float v[32];
+  for (; i0 + 64 <= E; i0 += 64) {
+    float v[64];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) v[j] = r.p[i0 + j];
+    for (int j = 0; j < 64; ++j) v[j] = r.p[i0 + j];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) sum = __fadd_rn(sum, v[j]);
+    for (int j = 0; j < 64; ++j) sum = __fadd_rn(sum, v[j]);
+  }
+  for (; i0 + 16 <= E; i0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = r.p[i0 + j];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sum = __fadd_rn(sum, v[j]);
   }
   for (; i0 < E; ++i0) sum = __fadd_rn(sum, r.p[i0]);
   __syncthreads();
@@ -143,16 +172,50 @@ G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *
     const float q = __fdiv_rn(r.p[i], sum);
     r.p[i] = q;
     nan |= q != q;
+    // group maxima (group i % K) of the probability bits, for the candidate filter
+    if (filter & (q == q)) atomicMax(&r.gmax[i % K], __float_as_uint(q));
   }
   // Top-k of Llama.kt:275-293 (K scans with strict >, the winner masked to -inf).
   // Without NaN every probability is finite and >= 0, and those scans pick the
   // elements in order of (larger value, then lower index): element i's rank is
   // the number of elements that beat it, computed by every thread for its own
-  // elements at once.  With a NaN present the scans themselves run (a NaN never
-  // wins; once nothing beats -inf the scan keeps index 0).
-  if (!__syncthreads_or(nan)) {
-    // (value, index) as one 64-bit key: p >= 0 is finite here, so its bits order
-    // as an unsigned integer, and the low word ranks lower indices higher
+  // elements at once.  (value, index) is one 64-bit key: the bits of p >= 0
+  // order as an unsigned integer, and the low word ranks lower indices higher.
+  // With a NaN present the scans themselves run (a NaN never wins; once nothing
+  // beats -inf the scan keeps index 0).
+  const bool any_nan = __syncthreads_or(nan);
+  if (!any_nan && filter) {
+    // The smallest of the K group maxima is at most the K-th largest probability
+    // (K distinct elements reach it), so the top K are among the elements at or
+    // above it, and every element that beats a candidate is a candidate too: a
+    // candidate's rank among the candidates is its rank among all E.
+    uint32_t t = 0xFFFFFFFFu;
+    for (int g = 0; g < K; ++g) t = min(t, r.gmax[g]);
+    for (int i = tid; i < E; i += 256) {
+      const uint32_t b = __float_as_uint(r.p[i]);
+      if (b >= t) r.key[atomicAdd(&r.n_cand, 1)] = ((uint64_t)b << 32) | (uint32_t)(~i);
+    }
+    __syncthreads();
+    const int n = r.n_cand;
+    for (int c = tid; c < n; c += 256) {
+      const uint64_t kc = r.key[c];
+      int r0 = 0, r1 = 0;
+      int d = 0;
+      for (; d + 8 <= n; d += 8) {
+        uint64_t kk[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) kk[u] = r.key[d + u];
+#pragma unroll
+        for (int u = 0; u < 8; u += 2) {
+          r0 += (int)(kk[u] > kc);
+          r1 += (int)(kk[u + 1] > kc);
+        }
+      }
+      for (; d < n; ++d) r0 += (int)(r.key[d] > kc);
+      const int rank = r0 + r1;
+      if (rank < K) r.pick_w[rank] = __uint_as_float((uint32_t)(kc >> 32)), r.pick_i[rank] = (int)~(uint32_t)kc;
+    }
+  } else if (!any_nan) {
     for (int i = tid; i < E; i += 256) r.key[i] = ((uint64_t)__float_as_uint(r.p[i]) << 32) | (uint32_t)(~i);
     __syncthreads();
     // element i's rank = number of keys above key[i]; `parts` threads share one
@@ -165,11 +228,18 @@ G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *
       int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
       const int j0 = part * E / parts, j1 = (part + 1) * E / parts;
       int j = j0;
-      for (; j + 4 <= j1; j += 4) {
-        r0 += (int)(r.key[j] > ki);
-        r1 += (int)(r.key[j + 1] > ki);
-        r2 += (int)(r.key[j + 2] > ki);
-        r3 += (int)(r.key[j + 3] > ki);
+      // 16 keys per LDS round trip: their reads go out before the compares
+      for (; j + 16 <= j1; j += 16) {
+        uint64_t kk[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) kk[u] = r.key[j + u];
+#pragma unroll
+        for (int u = 0; u < 16; u += 4) {
+          r0 += (int)(kk[u] > ki);
+          r1 += (int)(kk[u + 1] > ki);
+          r2 += (int)(kk[u + 2] > ki);
+          r3 += (int)(kk[u + 3] > ki);
+        }
       }
       for (; j < j1; ++j) r0 += (int)(r.key[j] > ki);
       int rank = (r0 + r1) + (r2 + r3);
@@ -233,6 +303,23 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   constexpr int wpb = 4;                         // launched with 256 threads
   const int gi = lane / LPR, q = lane % LPR;
   const int seg = blockIdx.y;
+  const int C = a.dim1 >> 6;
+  const float *x = a.x + (int64_t)(seg / a.x_div) * a.x_stride;
+  // x of a column pass, staged once per workgroup: each thread fetches XSEG
+  // 16-byte segments (coalesced); with the fused norm also the norm weights
+  u32x4a4 xr[XSEG];
+  u32x4a4 wr[NORM ? XSEG : 1];
+  auto load_x = [&](int pass) {
+#pragma unroll
+    for (int j = 0; j < XSEG; ++j) {
+      const int s = j * 256 + tid, c = pass * NCH + (s >> 4);
+      // dword alignment is all a caller's x guarantees; gfx950 takes 128-bit loads at that alignment
+      xr[j] = ((const u32x4a4 *)(x + (int64_t)(c < C ? c : 0) * 64))[s & 15];
+      if constexpr (NORM) wr[j] = ((const u32x4a4 *)(a.norm_w + (int64_t)(c < C ? c : 0) * 64))[s & 15];
+    }
+  };
+  // the routed launch has one column pass: its x is in flight while the token is routed
+  if constexpr (ROUTE) load_x(0);
   int expert = 0;
   if constexpr (ROUTE) {
     // the token's routing, computed by every workgroup of its segments (the
@@ -247,7 +334,6 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   }
   const bool bad_expert = (ROUTE || a.ids) && (expert < 0 || expert >= a.expert_count);
   const int64_t ebase = bad_expert ? 0 : (int64_t)expert * a.expert_stride;
-  const float *x = a.x + (int64_t)(seg / a.x_div) * a.x_stride;
   float *y = a.y ? a.y + (int64_t)seg * a.y_stride : nullptr;
 
   const int n_tiles = (a.rows + LRT - 1) / LRT;
@@ -256,7 +342,6 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   const int nwv = gridDim.x * wpb, wv = wid * gridDim.x + blockIdx.x;
   const int tpw = (n_tiles + nwv - 1) / nwv;
   const int t0 = min(n_tiles, wv * tpw), t1 = min(n_tiles, t0 + tpw);
-  const int C = a.dim1 >> 6;
   const int passes = MULTI ? (C + LPR * CPL - 1) / (LPR * CPL) : 1;
 
   // row (logical index, matrix, base) of tile t, step k for this lane's group
@@ -385,19 +470,10 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     uint32_t DA[RT][CPL][NDW], DB[RT][CPL][NDW];
     bool okA[RT][CPL], okB[RT][CPL];
     int64_t EA[RT][CPL], EB[RT][CPL];
-    // x of this pass, once per workgroup: each thread fetches XSEG 16-byte
-    // segments (coalesced), then the first weight tile goes out, and only then
+    // x of this pass goes out first, then the first weight tile, and only then
     // does the thread wait for x (vmcnt retires in issue order, so that wait
-    // never covers the weight latency; the barrier waits on LDS only).
-    u32x4a4 xr[XSEG];
-    u32x4a4 wr[NORM ? XSEG : 1];
-#pragma unroll
-    for (int j = 0; j < XSEG; ++j) {
-      const int s = j * 256 + tid, c = pass * NCH + (s >> 4);
-      // dword alignment is all a caller's x guarantees; gfx950 takes 128-bit loads at that alignment
-      xr[j] = ((const u32x4a4 *)(x + (int64_t)(c < C ? c : 0) * 64))[s & 15];
-      if constexpr (NORM) wr[j] = ((const u32x4a4 *)(a.norm_w + (int64_t)(c < C ? c : 0) * 64))[s & 15];
-    }
+    // never covers the weight latency; the barrier waits on LDS only)
+    if (!ROUTE) load_x(pass);
     load_tile(t0, pass, t0 < t1, DA, okA, EA);
     if (MULTI && pass > 0) __syncthreads();  // every wave has read the previous pass's x
     if constexpr (NORM) {
