@@ -359,6 +359,12 @@ int moe_dev(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t n_e
   b.x = d_h;
   b.x_stride = ff;
   b.x_div = 1;
+  // down and the weighted sum in one launch where the shape allows
+  g4::RowsArgs c = b;
+  c.y = d_Y;
+  c.y_stride = dim;
+  const hipError_t e = g4::launch_moe_down(wdn->type, c, d_w, T, k, ctx->dev, ctx->stream);
+  if (e != hipErrorNotSupported) return launch_status(e, "moe");
   b.y = d_ys;
   b.y_stride = dim;
   G4_TRY(launch_status(g4::launch_rows(wdn->type, g4::EPI_STORE, b, S, ctx->dev, nullptr, ctx->stream), "moe"));

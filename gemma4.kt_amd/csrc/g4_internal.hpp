@@ -103,6 +103,12 @@ hipError_t launch_argmax(const float *v, int32_t n, float *part_val, int32_t *pa
                          const DevInfo &dev, hipStream_t stream);
 hipError_t launch_route(const float *logits, int32_t T, int32_t n_experts, int32_t k, int32_t renorm,
                         const float *expert_scale, int32_t *ids, float *weights, hipStream_t stream);
+// Down projection and weighted sum of the routed experts in one launch for few
+// tokens (row tiles x tokens <= 2 per CU, k = 1..8, one column pass of at most
+// 2048 columns, rows on the 64-element fast path); hipErrorNotSupported otherwise
+// (the caller then uses launch_rows + launch_moe_combine).
+hipError_t launch_moe_down(int type, const RowsArgs &a, const float *gw, int32_t T, int32_t K, const DevInfo &dev,
+                           hipStream_t s);
 hipError_t launch_moe_combine(const float *ys, const float *weights, int32_t T, int32_t k, int32_t dim, float *Y,
                               hipStream_t stream);
 

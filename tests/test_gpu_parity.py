@@ -319,12 +319,14 @@ def test_moe_q4_k(g4, ctx, oracle, tokens):
 
 
 @pytest.mark.parametrize("case", ["t1", "t5", "t16", "ref_gates", "nan", "ties", "e256", "e300", "generic",
-                                  "k_all"])
+                                  "k_all", "k1", "k3", "k12", "ff2560", "rows100"])
 def test_moe_routed(g4, ctx, oracle, case):
     """g4_moe_routed: the routing runs inside the gate+up launch (up to 256 experts,
     rows on the 64-element fast path) or in a launch of its own (more experts, or
     the per-element path); either way the routing equals g4_moe_route's and the
-    oracle's exactly, and the output g4_moe's bit for bit."""
+    oracle's exactly, and the output g4_moe's bit for bit.  The down projection
+    and weighted sum share one launch for k <= 8 and ff <= 2048 (k1, k3: idle
+    waves; rows100: a partial row tile) and take two launches beyond (k12, ff2560)."""
     announce("moe routed %s" % case)
     E, D, FF, K, T, renorm, fmt = 16, 512, 256, 4, 3, True, Q4_K
     scale = None
@@ -341,6 +343,12 @@ def test_moe_routed(g4, ctx, oracle, case):
         D, FF = 96, 64      # gate+up rows of 96 elements: the per-element kernel
     elif case == "k_all":
         E, K = 8, 8
+    elif case in ("k1", "k3", "k12"):
+        K = int(case[1:])
+    elif case == "ff2560":
+        E, D, FF = 4, 128, 2560
+    elif case == "rows100":
+        D, FF = 100, 64
     gu = synth.weights(54, "gu" + case, fmt, E * 2 * FF * D)
     dn = synth.weights(54, "dn" + case, fmt, E * D * FF)
     lg = synth.activations(54, "lg" + case, T * E).reshape(T, E)
