@@ -580,11 +580,31 @@ G4_DEV void am_wave(float &v, int &i) {
 }
 
 
+// tanh(x) in double by fdlibm's algorithm (s_tanh.c), the one the JDK's
+// StrictMath.tanh (FdLibm.Tanh) runs and Math.tanh calls: |x| < 2^-55: x (1 + x);
+// |x| < 1: -t / (t + 2) with t = expm1(-2|x|); |x| < 22: 1 - 2 / (t + 2) with
+// t = expm1(2|x|); beyond: 1; then x's sign.  Near +-1, where gelu's 1 + tanh
+// keeps only the low bits, it is the correctly rounded double but in rare cases.
+G4_DEV double tanh_fdlibm(double x) {
+  const double ax = fabs(x);
+  if (x != x) return x + x;
+  if (ax < 0x1p-55) return x * (1.0 + x);
+  double z = 1.0;
+  if (ax < 1.0) {
+    const double t = expm1(-2.0 * ax);
+    z = -t / (t + 2.0);
+  } else if (ax < 22.0) {
+    const double t = expm1(2.0 * ax);
+    z = 1.0 - 2.0 / (t + 2.0);
+  }
+  return __builtin_signbit(x) ? -z : z;
+}
+
 // Llama.kt:23-25 gelu, evaluated in double like the reference.
 G4_DEV float gelu_ref(float xf) {
   double x = (double)xf;
   double inner = 0.7978845608028654 * (x + 0.044715 * (x * x * x));
-  return (float)(0.5 * x * (1.0 + tanh(inner)));
+  return (float)(0.5 * x * (1.0 + tanh_fdlibm(inner)));
 }
 
 // ------------------------------------------------------------ rms norm ----
@@ -625,7 +645,7 @@ G4_DEV float block_sum256(float v, float *red) {
 
 // Llama.kt:403-406 final logit soft-capping: cap * (float)tanh((double)(v / cap)).
 G4_DEV float softcap_ref(float v, float cap) {
-  return __fmul_rn(cap, (float)tanh((double)__fdiv_rn(v, cap)));
+  return __fmul_rn(cap, (float)tanh_fdlibm((double)__fdiv_rn(v, cap)));
 }
 
 }  // namespace g4

@@ -586,11 +586,30 @@ void or_route(const float *logits, int32_t n_experts, int32_t k, int renormalize
   free(p);
 }
 
+/* kotlin.math.tanh = java.lang.Math.tanh, which calls StrictMath.tanh: fdlibm's
+   algorithm (s_tanh.c; the JDK's FdLibm.Tanh): |x| < 2^-55: x * (1 + x);
+   |x| < 1: -t / (t + 2), t = expm1(-2|x|); |x| < 22: 1 - 2 / (t + 2),
+   t = expm1(2|x|); beyond: 1; then x's sign.  expm1 is the C library's. */
+double or_tanh(double x) {
+  const double ax = fabs(x);
+  double z = 1.0;
+  if (isnan(x)) return x + x;
+  if (ax < 0x1p-55) return x * (1.0 + x);
+  if (ax < 1.0) {
+    const double t = expm1(-2.0 * ax);
+    z = -t / (t + 2.0);
+  } else if (ax < 22.0) {
+    const double t = expm1(2.0 * ax);
+    z = 1.0 - 2.0 / (t + 2.0);
+  }
+  return signbit(x) ? -z : z;
+}
+
 /* Llama.kt:23-25: (0.5 * x * (1 + tanh(sqrt(2/PI) * (x + 0.044715 * x^3)))).toFloat(). */
 float or_gelu(float xf) {
   double x = (double)xf;
   double inner = sqrt(2.0 / 3.141592653589793) * (x + 0.044715 * pow(x, 3.0));
-  return (float)(0.5 * x * (1.0 + tanh(inner)));
+  return (float)(0.5 * x * (1.0 + or_tanh(inner)));
 }
 
 /* ---------------------------------------------------------------- MoE ---- */
@@ -641,7 +660,7 @@ void or_moe_exact(int type_gu, const uint8_t *gate_up, int type_dn, const uint8_
                       nthreads);
       for (int32_t i = 0; i < ff; i++) {
         double g = gu[i], u = gu[ff + i];
-        double gl = 0.5 * g * (1.0 + tanh(sqrt(2.0 / 3.141592653589793) * (g + 0.044715 * g * g * g)));
+        double gl = 0.5 * g * (1.0 + or_tanh(sqrt(2.0 / 3.141592653589793) * (g + 0.044715 * g * g * g)));
         h[i] = gl * u;
         /* error scale of h in units of 1e-5: 1.2*Sg*(|u| + 1e-5*Su) + |gelu(g)|*Su, plus fp32 rounding of h */
         hb[i] = 1.2 * gua[i] * (fabs(u) + 1e-5 * gua[ff + i]) + fabs(gl) * gua[ff + i] + fabs(h[i]) * 0.05;
@@ -704,7 +723,7 @@ void or_rmsnorm_exact(double *out, const float *x, const float *w, int32_t size,
 void or_softcap(float *v, int32_t n, float cap) {
   for (int32_t i = 0; i < n; i++) {
     float q = v[i] / cap;
-    float t = (float)tanh((double)q);
+    float t = (float)or_tanh((double)q);
     v[i] = cap * t;
   }
 }
@@ -773,7 +792,7 @@ void or_ffn_block_exact(int type_g, const uint8_t *gate, int type_u, const uint8
   mv_exact64(type_u, up, xb, NULL, u, au, NULL, hidden, dim, nthreads);
   for (int32_t i = 0; i < hidden; i++) {
     double gi = g[i];
-    double gl = 0.5 * gi * (1.0 + tanh(sqrt(2.0 / 3.141592653589793) * (gi + 0.044715 * gi * gi * gi)));
+    double gl = 0.5 * gi * (1.0 + or_tanh(sqrt(2.0 / 3.141592653589793) * (gi + 0.044715 * gi * gi * gi)));
     h[i] = gl * u[i];
     /* g and u are off by their dot error plus the carried norm error: 2 * sum |w xb| */
     double bg = 2.0 * ag[i], bu = 2.0 * au[i];
@@ -819,7 +838,7 @@ void or_lm_head_exact(int type, const uint8_t *w, const float *norm, const float
   mv_exact64(type, w, xb, NULL, logits64, bound64, NULL, vocab, dim, nthreads);
   for (int32_t i = 0; i < vocab; i++) {
     bound64[i] *= 2.0;
-    if (cap > 0.0f) logits64[i] = (double)cap * tanh(logits64[i] / (double)cap);
+    if (cap > 0.0f) logits64[i] = (double)cap * or_tanh(logits64[i] / (double)cap);
     bound64[i] += 0.05 * fabs(logits64[i]);
   }
   free(xb);

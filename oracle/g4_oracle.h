@@ -102,6 +102,8 @@ void or_topk(float *probs, int32_t n, int32_t k, int32_t *idx_out, float *val_ou
  * (Llama.kt:300-304 finalWeight = prob * downScale). */
 void or_route(const float *logits, int32_t n_experts, int32_t k, int renormalize,
               const float *expert_scale, int32_t *ids, float *weights);
+/* Math.tanh as StrictMath.tanh computes it (fdlibm's algorithm, the C library's expm1). */
+double or_tanh(double x);
 /* Llama.kt:23-25 gelu (tanh form, evaluated in double). */
 float or_gelu(float x);
 

@@ -39,6 +39,7 @@ _SIG = {
     "or_topk": ([_vp, _i32, _i32, _vp, _vp], None),
     "or_route": ([_vp, _i32, _i32, ctypes.c_int, _vp, _vp, _vp], None),
     "or_gelu": ([ctypes.c_float], ctypes.c_float),
+    "or_tanh": ([ctypes.c_double], ctypes.c_double),
     "or_moe": ([ctypes.c_int, _vp, ctypes.c_int, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, ctypes.c_int,
                 ctypes.c_int], None),
     "or_moe_exact": ([ctypes.c_int, _vp, ctypes.c_int, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _vp,
@@ -219,6 +220,11 @@ def route(logits, k: int, renormalize: bool, expert_scale=None):
 
 def gelu(x: float) -> float:
     return lib().or_gelu(x)
+
+
+def tanh(x: float) -> float:
+    """Math.tanh as StrictMath.tanh computes it (fdlibm's algorithm)."""
+    return lib().or_tanh(x)
 
 
 def moe(t_gu: int, gate_up, t_dn: int, down, X, ids, w, dim: int, ff: int, mode: int = MODE_VECTOR,

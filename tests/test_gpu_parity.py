@@ -203,6 +203,30 @@ def _ffn_reference(oracle, c):
     return y64[0], bound[0]
 
 
+def test_gelu_through_identity_gate_up(g4, ctx, oracle):
+    """gelu itself (Llama.kt:23-25, tanh of StrictMath.tanh in double): with BF16
+    identity gate and up matrices, h_i = gelu(x_i) * x_i exactly, so h is compared
+    bit for bit with the oracle's gelu over x spanning its regimes (cancellation of
+    1 + tanh near x = -6, saturation, tiny and huge x).  The device's expm1 and the
+    C library's may differ in a last bit, which reaches the float result only in
+    rare halfway cases."""
+    announce("gelu through identity gate/up")
+    n = 4096
+    rng = np.random.default_rng(63)
+    x = np.concatenate([np.linspace(-12, 12, n // 2), 10.0 ** rng.uniform(-30, 1.5, n // 2 - 8) *
+                        rng.choice([-1.0, 1.0], n // 2 - 8),
+                        [0.0, -0.0, 1e-40, -1e-40, 3e38, -3e38, 40.0, -40.0]]).astype(np.float32)
+    eye = np.zeros((n, n), np.uint16)
+    eye[np.arange(n), np.arange(n)] = 0x3F80  # bf16 1.0
+    w = upload(g4, ctx, BF16, eye.view(np.uint8).reshape(-1), n * n)
+    h = g4.ffn_gate_up(ctx, w, w, x, n, n)
+    with np.errstate(over="ignore"):  # gelu(3e38) * 3e38 overflows to inf on both sides
+        ref = np.array([np.float32(oracle.gelu(float(v))) * v for v in x], np.float32)
+    fin = np.isfinite(ref)
+    assert np.count_nonzero(h[fin].view(np.uint32) != ref[fin].view(np.uint32)) <= 1
+    assert same_bits(h[~fin], ref[~fin])
+
+
 def test_q4_0_ffn_one_token(g4, ctx, oracle):
     announce("workload q4_0 ffn 8192x2048")
     c = synth.q4_0_ffn()

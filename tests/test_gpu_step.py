@@ -11,8 +11,9 @@ Bars (written into each check):
     sequential one);
   * residual add: bit-exact;
   * soft-capping: within 2 ulp of cap * tanh(v / cap) evaluated in fp64 (the
-    reference rounds a double tanh to float; libm and device tanh may differ in
-    the last double bits);
+    reference rounds a double tanh to float; the oracle and the device both run
+    fdlibm's tanh, over the C library's and the device's own expm1, which may
+    differ in a last double bit);
   * norm fused into the matvec: bit-identical to the standalone norm followed by
     the plain matvec, and every dot within 1e-5 * sum |w_i xn_i|;
   * blocks: within the error bound the fp64 oracle carries through the block
@@ -152,7 +153,7 @@ def test_softcap(g4, ctx, oracle, dev):
     ulp = np.spacing(np.abs(ref))
     assert np.all(np.abs(got[fin].astype(np.float64) - ref) <= 2 * ulp)
     assert same_bits(got[~fin], oracle.softcap(v[~fin], cap))
-    # the oracle (libm tanh) and the device agree except, rarely, in the last bit
+    # the oracle and the device agree except, rarely, in the last bit (expm1)
     orc = oracle.softcap(v, cap)
     assert np.count_nonzero(got[fin] != orc[fin]) <= v.size // 10000
 

@@ -344,6 +344,33 @@ def test_gelu_matches_torch_tanh_form(oracle):
     assert np.all(np.abs(ours - ref) <= 2e-7 * np.abs(ref) + 1e-12)
 
 
+def test_tanh_is_fdlibms_within_an_ulp(oracle):
+    """or_tanh restates StrictMath.tanh (fdlibm's algorithm, what Math.tanh calls).
+    Pinned against mpmath at 60 digits: within 2 ulps everywhere (Math.tanh's
+    contract allows 2.5), odd, and the special values; near -1 (where gelu's
+    1 + tanh keeps only the low bits) it is the correctly rounded double."""
+    mpmath = pytest.importorskip("mpmath")
+    mpmath.mp.dps = 60
+    rng = np.random.default_rng(62)
+    xs = np.concatenate([10.0 ** rng.uniform(-20, np.log10(30.0), 3000), np.linspace(0.0, 25.0, 501),
+                         [2.0 ** -55, np.nextafter(2.0 ** -55, 0), 1.0, np.nextafter(1.0, 0), 22.0,
+                          np.nextafter(22.0, 0)]])
+    for x in xs:
+        x = float(x)
+        got = oracle.tanh(x)
+        exact = mpmath.tanh(mpmath.mpf(x))
+        ulp = np.spacing(abs(float(exact))) if exact != 0 else 5e-324
+        assert abs(mpmath.mpf(got) - exact) <= 2 * ulp, x
+        assert oracle.tanh(-x) == -got
+    cr = 0
+    for z in np.linspace(2.0, 8.0, 2001):
+        cr += oracle.tanh(-float(z)) == float(mpmath.tanh(mpmath.mpf(-float(z))))
+    assert cr >= 1990
+    assert oracle.tanh(np.inf) == 1.0 and oracle.tanh(-np.inf) == -1.0 and np.isnan(oracle.tanh(np.nan))
+    assert oracle.tanh(30.0) == 1.0 and oracle.tanh(1e-300) == 1e-300
+    assert np.signbit(oracle.tanh(-0.0)) and oracle.tanh(-0.0) == 0.0
+
+
 # ---------------------------------------------------------------- mutations ---
 # The comparisons above must fail for plausible mistakes; plant each mistake in a
 # copy of the numpy restatement and check the oracle disagrees with it.
