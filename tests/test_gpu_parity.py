@@ -342,15 +342,17 @@ def test_moe_q4_k(g4, ctx, oracle, tokens):
     assert same_bits(Yr, Y)
 
 
-@pytest.mark.parametrize("case", ["t1", "t5", "t16", "ref_gates", "nan", "ties", "e256", "e300", "generic",
-                                  "k_all", "k1", "k3", "k12", "ff2560", "rows100"])
+@pytest.mark.parametrize("case", ["t1", "t5", "t16", "ref_gates", "nan", "ties", "near_ties", "e256", "e300",
+                                  "generic", "k_all", "k1", "k3", "k12", "ff2560", "rows100"])
 def test_moe_routed(g4, ctx, oracle, case):
     """g4_moe_routed: the routing runs inside the gate+up launch (up to 256 experts,
     rows on the 64-element fast path) or in a launch of its own (more experts, or
     the per-element path); either way the routing equals g4_moe_route's and the
     oracle's exactly, and the output g4_moe's bit for bit.  The down projection
     and weighted sum share one launch for k <= 8 and ff <= 2048 (k1, k3: idle
-    waves; rows100: a partial row tile) and take two launches beyond (k12, ff2560)."""
+    waves; rows100: a partial row tile) and take two launches beyond (k12, ff2560).
+    near_ties: distinct logits whose probabilities round to one value, so the
+    probabilities rank by index where the logits rank the other way."""
     announce("moe routed %s" % case)
     E, D, FF, K, T, renorm, fmt = 16, 512, 256, 4, 3, True, Q4_K
     scale = None
@@ -382,6 +384,9 @@ def test_moe_routed(g4, ctx, oracle, case):
     elif case == "ties":
         lg[:, :] = np.round(lg * 2) / 2
         lg[0, :] = 1.0
+    elif case == "near_ties":
+        lg[:, :] = (np.arange(E) * 1e-9).astype(np.float32)   # exp rounds every difference away
+        lg[1, ::3] = 0.5                                      # and a token with clear winners too
     wgu = upload(g4, ctx, fmt, gu, E * 2 * FF * D)
     wdn = upload(g4, ctx, fmt, dn, E * D * FF)
     Yr, idr, wr = g4.moe_routed(ctx, wgu, wdn, X, lg, K, renorm, D, FF, scale)
