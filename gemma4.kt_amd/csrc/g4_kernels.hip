@@ -14,6 +14,8 @@
 #include <float.h>
 #include <limits.h>
 
+#include <atomic>
+
 #include "../../include/g4hip.h"
 #include "g4_device.hpp"
 #include "g4_internal.hpp"
@@ -915,12 +917,16 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
 
   // Resident 256-thread workgroups per CU for this kernel (register-limited);
   // the launch fills exactly that many waves when there are tiles enough.
-  static int resident[3][2][2][2];
-  int &res = resident[epi][multi ? 1 : 0][norm ? 1 : 0][route ? 1 : 0];
+  // Looked up once per kernel; contexts on other threads may race to store the
+  // same value, hence relaxed atomics.
+  static std::atomic<int> resident[3][2][2][2];
+  std::atomic<int> &slot = resident[epi][multi ? 1 : 0][norm ? 1 : 0][route ? 1 : 0];
+  int res = slot.load(std::memory_order_relaxed);
   if (res == 0) {
     int nb = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 256, 0) != hipSuccess || nb < 1) nb = 2;
     res = nb;
+    slot.store(res, std::memory_order_relaxed);
   }
   const int lrt = epi == EPI_GELU_PAIR ? TR / 2 : TR;
   const int64_t n_tiles = (a.rows + lrt - 1) / lrt;

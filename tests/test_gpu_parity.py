@@ -166,6 +166,65 @@ def test_matmul_dev_matches_host(g4, ctx, oracle):
     assert same_bits(yd.cpu().numpy(), y)
 
 
+def test_concurrent_contexts_share_weights(g4, ctx, oracle):
+    """Several generate calls may run at once on one model (GemmaModel.kt:73): four
+    threads, each with its own context, run matmul (Q4_K and Q8_0) and the routed MoE
+    on weights uploaded once, at the same time (ctypes drops the GIL during the
+    calls).  Every result equals the one the same call gives alone, bit for bit."""
+    import threading
+    announce("concurrent contexts")
+    dim0, dim1 = 1024, 2048
+    raw_k = synth.weights(57, "ck", Q4_K, dim0 * dim1)
+    raw_8 = synth.weights(57, "c8", Q8_0, dim0 * dim1)
+    wk = upload(g4, ctx, Q4_K, raw_k, dim0 * dim1)
+    w8 = upload(g4, ctx, Q8_0, raw_8, dim0 * dim1)
+    E, D, FF, K = 16, 512, 256, 4
+    gu = synth.q4_k(57, "gu", E * 2 * FF * D)
+    dn = synth.q4_k(57, "dn", E * D * FF)
+    wgu = upload(g4, ctx, Q4_K, gu, E * 2 * FF * D)
+    wdn = upload(g4, ctx, Q4_K, dn, E * D * FF)
+    xs = [synth.activations(57, "x%d" % i, dim1) for i in range(6)]
+    lgs = [synth.activations(57, "lg%d" % i, 2 * E).reshape(2, E) for i in range(6)]
+    Xs = [synth.activations(57, "X%d" % i, 2 * D).reshape(2, D) for i in range(6)]
+    alone = []
+    for i in range(6):
+        yk = np.empty(dim0, np.float32)
+        y8 = np.empty(dim0, np.float32)
+        wk.matmul(xs[i], yk, dim0, dim1)
+        w8.matmul(xs[i], y8, dim0, dim1)
+        Y, ids, gw = g4.moe_routed(ctx, wgu, wdn, Xs[i], lgs[i], K, True, D, FF)
+        alone.append((yk, y8, Y, ids, gw))
+    lib = g4.lib()
+    bad = []
+
+    def worker(k):
+        c = g4.Context(0)
+        try:
+            for it in range(12):
+                i = (k + it) % 6
+                yk = np.empty(dim0, np.float32)
+                y8 = np.empty(dim0, np.float32)
+                g4.check(lib.g4_matmul(c.handle, wk.handle, 0, xs[i].ctypes.data, yk.ctypes.data, dim0, dim1))
+                g4.check(lib.g4_matmul(c.handle, w8.handle, 0, xs[i].ctypes.data, y8.ctypes.data, dim0, dim1))
+                Y, ids, gw = g4.moe_routed(c, wgu, wdn, Xs[i], lgs[i], K, True, D, FF)
+                ref = alone[i]
+                if not (same_bits(yk, ref[0]) and same_bits(y8, ref[1]) and same_bits(Y, ref[2])
+                        and np.array_equal(ids, ref[3]) and same_bits(gw, ref[4])):
+                    bad.append((k, it))
+        except Exception as e:  # reported below, in the test's thread
+            bad.append((k, repr(e)))
+        finally:
+            c.close()
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=100)
+    assert not any(t.is_alive() for t in threads)
+    assert not bad, bad[:5]
+
+
 def test_range_errors_on_device(g4, ctx):
     announce("range errors")
     raw = synth.weights(45, "err", Q8_0, 64 * 32)
