@@ -458,6 +458,30 @@ def test_moe_routed(g4, ctx, oracle, case):
     assert_dots(Yr.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe routed %s" % case)
 
 
+@pytest.mark.parametrize("fmt", [Q4_K, Q8_0])
+def test_moe_batch_equals_tokens_alone(g4, ctx, oracle, fmt):
+    """A batch of tokens gives every token the bits it gets alone: alone a token's
+    down projection and weighted sum share one launch, in a batch of 16 they take
+    the per-pair down launch and the combine; ids chosen by three or more pairs of
+    the batch included."""
+    announce("moe batch vs alone fmt=%d" % fmt)
+    E, D, FF, K, T = 16, 512, 256, 4, 16
+    gu = synth.weights(58, "gu", fmt, E * 2 * FF * D)
+    dn = synth.weights(58, "dn", fmt, E * D * FF)
+    lg = synth.activations(58, "lg", T * E).reshape(T, E)
+    X = synth.activations(58, "X", T * D).reshape(T, D)
+    wgu = upload(g4, ctx, fmt, gu, E * 2 * FF * D)
+    wdn = upload(g4, ctx, fmt, dn, E * D * FF)
+    Yb, idb, wb = g4.moe_routed(ctx, wgu, wdn, X, lg, K, True, D, FF)
+    assert max(np.bincount(idb.reshape(-1))) >= 3
+    for t in range(T):
+        Y1, id1, w1 = g4.moe_routed(ctx, wgu, wdn, X[t:t + 1], lg[t:t + 1], K, True, D, FF)
+        assert np.array_equal(id1[0], idb[t]) and same_bits(w1[0], wb[t]), t
+        assert same_bits(Y1[0], Yb[t]), t
+    y64, bound = oracle.moe_exact(fmt, gu, fmt, dn, X, idb, wb, D, FF)
+    assert_dots(Yb.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe batch")
+
+
 def test_moe_routed_dev_calls(g4, ctx, oracle):
     """The device entry point on resident buffers, twice in a row with fewer tokens
     the second time: ids, weights and Y of each call match the host entry point."""
