@@ -888,6 +888,12 @@ bool rows_norm_ok(int type, const RowsArgs &a, bool paired) {
 
 int max_argmax_blocks(const DevInfo &dev) { return dev.cu_count * 8; }
 
+// A format's tiles with one row step (F::RT = 1): more, smaller tiles.
+template <class F>
+struct OneStep : F {
+  static constexpr int RT = 1;
+};
+
 template <class F, int LPR, int CPL>
 static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, const DevInfo &dev, hipStream_t s) {
   constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1, RPW = 64 / LPR, TR = RT * RPW;
@@ -962,6 +968,17 @@ static hipError_t launch_fast(int epi, const RowsArgs &a, int segments, const De
   const int C = a.dim1 / 64;
   // single column pass up to 64 lanes x 2 chunks = 8192 columns; passes beyond that
   if (C > 64 && epi != EPI_GELU_PAIR) return launch_fast_cfg<F, 64, 2>(epi, a, segments, dev, s);
+  // Q8_0 and Q6_K (the formats with the widest chunks, 17 and 29 dwords) take
+  // one row step per tile up to 16384 rows: measured 4.55 -> 4.30 us on the
+  // 2048-row Q8_0 matvec and 8.04 -> 7.31 us on the 8192-row Q6_K one, while
+  // Q4_K got slower and the 262144-row LM head lost 1.4 us with it
+  if constexpr (F::RT >= 2 && (F::TYPE == T_Q8_0 || F::TYPE == T_Q6_K)) {
+    if (epi == EPI_STORE && (int64_t)a.rows * segments <= 16384) {
+      if (C > 32) return launch_fast_cfg<OneStep<F>, 64, 1>(epi, a, segments, dev, s);
+      if (C > 16) return launch_fast_cfg<OneStep<F>, 32, 1>(epi, a, segments, dev, s);
+      return launch_fast_cfg<OneStep<F>, 16, 1>(epi, a, segments, dev, s);
+    }
+  }
   if (C > 32) return launch_fast_cfg<F, 64, 1>(epi, a, segments, dev, s);
   if (C > 16) return launch_fast_cfg<F, 32, 1>(epi, a, segments, dev, s);
   return launch_fast_cfg<F, 16, 1>(epi, a, segments, dev, s);
