@@ -290,6 +290,9 @@ int check_moe(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t T
   G4_TRY(check_weight(ctx, wgu, "w_gate_up"));
   G4_TRY(check_weight(ctx, wdn, "w_down"));
   if (T < 0 || k < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative T or k (%d, %d)", T, k);
+  // one launch row of workgroups per (token, slot) pair
+  if ((int64_t)T * k > 65535)
+    return fail(G4_ERR_INVALID_ARGUMENT, "T*k = %lld (token, slot) pairs exceed 65535 per call", (long long)T * k);
   if (dim <= 0 || ff <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "moe dims must be positive (%d, %d)", dim, ff);
   const int64_t per_gu = 2 * (int64_t)ff * dim, per_dn = (int64_t)dim * ff;
   if (wgu->n_elems % per_gu != 0)

@@ -239,6 +239,12 @@ def test_range_errors_on_device(g4, ctx):
         g4.FloatTensorFactory.create(ctx, Q8_0, raw[:100], 64 * 32)
     with pytest.raises(g4.UnsupportedOperationException):
         g4.FloatTensorFactory.create(ctx, 3, raw, 64 * 32)
+    # MoE: more (token, slot) pairs than one launch takes, checked before any copy
+    gu = synth.weights(45, "egu", Q8_0, 2 * 2 * 32 * 64)
+    wgu = upload(g4, ctx, Q8_0, gu, 2 * 2 * 32 * 64)
+    wdn = upload(g4, ctx, Q8_0, gu[: gu.size // 2], 2 * 32 * 64)
+    with pytest.raises(g4.IllegalArgumentException):
+        g4.moe_dev(ctx, wgu, wdn, 0, 32769, 64, 32, 0, 0, 2, 0)
 
 
 # -------------------------------------------------------------- workloads ---
