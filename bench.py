@@ -95,6 +95,10 @@ class Workload:
         """Launch only the dominant kernel of step i (for its roofline timing)."""
         self.step(i)
 
+    # The same step through the host-pointer entry point (activations copied in,
+    # results copied out, synchronous), timed apart from `value`; None: no such call.
+    host_step = None
+
     def cpu_step(self) -> None:
         raise NotImplementedError
 
@@ -133,6 +137,10 @@ class FfnQ4_0(Workload):
         self.g4.ffn_gate_up_dev(self.ctx, wg, wu, self.x, self.h, self.dim, self.hidden)
         wd.matmul_dev(self.h, self.y, self.dim, self.hidden)
 
+    def host_step(self, i):
+        wg, wu, wd = self.w[i % self.copies]
+        self.g4.ffn(self.ctx, wg, wu, wd, self.c["x"], self.dim, self.hidden)
+
     def dominant(self, i):
         wg, wu, _ = self.w[i % self.copies]
         self.g4.ffn_gate_up_dev(self.ctx, wg, wu, self.x, self.h, self.dim, self.hidden)
@@ -165,11 +173,15 @@ class MatvecQ8_0(Workload):
         self.w = [g4.FloatTensorFactory.create(ctx, Q8_0, c["w"], 2048 * 2048) for _ in range(self.copies)]
         self.x = torch.from_numpy(c["x"]).cuda()
         self.y = torch.empty(2048, dtype=torch.float32, device="cuda")
+        self.yh = np.empty(2048, np.float32)
         self.step_bytes = c["w"].nbytes + 4 * 2048 * 2
         self.dominant_bytes = self.step_bytes
 
     def step(self, i):
         self.w[i % self.copies].matmul_dev(self.x, self.y, 2048, 2048)
+
+    def host_step(self, i):
+        self.w[i % self.copies].matmul(self.c["x"], self.yh, 2048, 2048)
 
     def cpu_setup(self, oracle):
         self.oracle = oracle
@@ -197,11 +209,15 @@ class LmHeadQ8_0(Workload):
         self.x = torch.from_numpy(c["x"]).cuda()
         self.logits = torch.empty(V, dtype=torch.float32, device="cuda")
         self.idx = torch.zeros(1, dtype=torch.int32, device="cuda")
+        self.lh = np.empty(V, np.float32)
         self.step_bytes = c["w"].nbytes + 4 * D + 4 * V + 4
         self.dominant_bytes = self.step_bytes
 
     def step(self, i):
         self.w[i % self.copies].matmul_argmax_dev(self.x, self.logits, self.idx.data_ptr(), self.V, self.D)
+
+    def host_step(self, i):
+        self.w[i % self.copies].matmul_argmax(self.c["x"], self.V, self.D, logits=self.lh)
 
     def cpu_setup(self, oracle):
         self.oracle = oracle
@@ -248,6 +264,9 @@ class BatchedQ4_K(Workload):
     def step(self, i):
         self.w[i % self.copies].matmul_batch_dev(self.X, self.m, self.Y, self.R, self.D)
 
+    def host_step(self, i):
+        self.w[i % self.copies].matmul_batch(np.ascontiguousarray(self.c["x"]), self.R, self.D)
+
     def cpu_setup(self, oracle):
         self.oracle = oracle
 
@@ -277,7 +296,7 @@ class MoeQ4_K(Workload):
         self.wgu = g4.FloatTensorFactory.create(ctx, Q4_K, base["gate_up"], E * 2 * FF * D)
         self.wdn = g4.FloatTensorFactory.create(ctx, Q4_K, base["down"], E * D * FF)
         self.copies = routings
-        self.logits, self.X, self.distinct = [], [], []
+        self.logits, self.X, self.distinct, self.lgh, self.Xh = [], [], [], [], []
         for r in range(routings):  # routing r = the logits/x streams of synth.moe_q4_k(tokens, routing_seed=r)
             lg = synth.activations(synth.SEED_MOE_Q4_K, "router%d.%d" % (tokens, r), tokens * E).reshape(tokens, E)
             x = synth.activations(synth.SEED_MOE_Q4_K, "x%d.%d" % (tokens, r), tokens * D).reshape(tokens, D)
@@ -285,6 +304,8 @@ class MoeQ4_K(Workload):
             self.distinct.append(len(np.unique(ids)))
             self.logits.append(torch.from_numpy(lg).cuda())
             self.X.append(torch.from_numpy(x).cuda())
+            self.lgh.append(lg)
+            self.Xh.append(x)
         self.ids = torch.zeros((tokens, K), dtype=torch.int32, device="cuda")
         self.gw = torch.zeros((tokens, K), dtype=torch.float32, device="cuda")
         self.Y = torch.empty((tokens, D), dtype=torch.float32, device="cuda")
@@ -303,6 +324,10 @@ class MoeQ4_K(Workload):
         r = i % self.copies
         self.g4.moe_routed_dev(self.ctx, self.wgu, self.wdn, self.X[r], self.T, self.D, self.FF, self.logits[r],
                                self.E, self.K, True, self.ids.data_ptr(), self.gw, self.Y)
+
+    def host_step(self, i):
+        r = i % self.copies
+        self.g4.moe_routed(self.ctx, self.wgu, self.wdn, self.Xh[r], self.lgh[r], self.K, True, self.D, self.FF)
 
     def cpu_setup(self, oracle):
         self.oracle = oracle
@@ -336,11 +361,15 @@ class MatvecKQuant(Workload):
         self.w = [g4.FloatTensorFactory.create(ctx, ggml_type, self.raw, self.R * self.D) for _ in range(self.copies)]
         self.x = torch.from_numpy(self.xh).cuda()
         self.y = torch.empty(self.R, dtype=torch.float32, device="cuda")
+        self.yh = np.empty(self.R, np.float32)
         self.step_bytes = self.dominant_bytes = self.raw.nbytes + 4 * (self.D + self.R)
         self.fmt = fmt
 
     def step(self, i):
         self.w[i % self.copies].matmul_dev(self.x, self.y, self.R, self.D)
+
+    def host_step(self, i):
+        self.w[i % self.copies].matmul(self.xh, self.yh, self.R, self.D)
 
     def cpu_setup(self, oracle):
         self.oracle = oracle
@@ -389,6 +418,11 @@ class FfnBlockQ4_0(Workload):
         self.g4.ffn_block_dev(self.ctx, wg, wu, wd, self.n_pre, self.n_post, self.x, self.dim, self.hidden,
                               self.eps)
 
+    def host_step(self, i):
+        wg, wu, wd = self.w[i % self.copies]
+        self.g4.ffn_block(self.ctx, wg, wu, wd, self.n_pre, self.n_post, self.c["x"], self.dim, self.hidden,
+                          self.eps)
+
     def cpu_setup(self, oracle):
         self.oracle = oracle
 
@@ -428,6 +462,10 @@ class LmHeadCapQ8_0(LmHeadQ8_0):
     def step(self, i):
         self.g4.lm_head_dev(self.ctx, self.w[i % self.copies], self.norm, self.x, self.logits,
                             self.idx.data_ptr(), self.V, self.D, self.eps, self.cap)
+
+    def host_step(self, i):
+        self.g4.lm_head(self.ctx, self.w[i % self.copies], self.norm, self.c["x"], self.V, self.D, self.eps,
+                        self.cap)
 
     def cpu_step(self):
         self.cpu_step_rows(self.V)
@@ -630,6 +668,17 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool)
         launches = dom_rounds * copies
         kern_ms = ev0.elapsed_time(ev1) / launches
         ctx.set_stream(None)
+    # the host-pointer entry point of the same step (copies in and out, synchronous;
+    # not part of `value`): after a few untimed calls, the mean over whole passes
+    host_us = None
+    if wl.host_step is not None:
+        for i in range(min(wl.copies, 4)):
+            wl.host_step(i)
+        n_host = wl.copies * max(1, math.ceil(16 / wl.copies))
+        t0 = time.perf_counter()
+        for i in range(n_host):
+            wl.host_step(i)
+        host_us = (time.perf_counter() - t0) / n_host * 1e6
     ms_per_step = elapsed * 1e3 / steps
     if wl.unit == "tokens/s":
         value = wl.tokens_per_step / (ms_per_step / 1e3)
@@ -664,6 +713,12 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool)
         "data": "synthetic: seeded GGUF blocks and activations (gemma4.kt_amd/synth.py)",
         "config": dict(wl.config(), graph=step_graph is not None, step_gbs=round(gbs_step, 2),
                        hbm_fraction=round(gbs_step / HBM_PEAK_GBS, 4)),
+        # host-pointer calls (activations over PCIe each call), reported apart from value
+        "host_pointer_call": None if host_us is None else {
+            "us_per_step": round(host_us, 2),
+            "value": round((wl.tokens_per_step if wl.unit == "tokens/s" else wl.step_bytes / 1e9) / (host_us / 1e6),
+                           3),
+            "unit": wl.unit},
         "roofline": roofline,
     }
     if cpu_seconds > 0 and not isinstance(wl, CopyCalibration):
