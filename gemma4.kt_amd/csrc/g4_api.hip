@@ -15,6 +15,13 @@
 #include "../../include/g4hip.h"
 #include "g4_internal.hpp"
 
+// A result of a host-pointer call waiting in pinned memory for the call's end.
+struct G4PendingOut {
+  void *dst;
+  const char *src;
+  size_t bytes;
+};
+
 struct g4_ctx {
   int device;
   hipStream_t own_stream;
@@ -25,6 +32,14 @@ struct g4_ctx {
   float *am_val;  // per-block argmax partials and a result slot
   int32_t *am_idx;
   int32_t *am_out;
+  // Host-pointer calls: activations and results pass through pinned host memory
+  // (grow-only), moved by a copy kernel; results reach the caller's arrays when
+  // the call ends (finish).
+  char *pin;
+  size_t pin_bytes;
+  size_t pin_used;
+  G4PendingOut outs[8];
+  int n_outs;
 };
 
 struct g4_weight {
@@ -83,6 +98,13 @@ size_t up(size_t n) { return (n + ALIGN - 1) & ~(ALIGN - 1); }
 
 int use_device(g4_ctx *ctx) {
   G4_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  // a host-pointer call that failed part way leaves staged results behind: they
+  // are dropped (the call reported its error) once its queued work is done
+  if (ctx->pin_used || ctx->n_outs) {
+    G4_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    ctx->pin_used = 0;
+    ctx->n_outs = 0;
+  }
   return G4_OK;
 }
 
@@ -165,18 +187,89 @@ int launch_status(hipError_t e, const char *what) {
   return G4_OK;
 }
 
+// Activations up to this size go through pinned memory and the copy kernel;
+// larger ones take the DMA engines.
+constexpr size_t PIN_MAX_COPY = size_t(256) << 10;
+
+void flush_outs(g4_ctx *ctx) {
+  for (int i = 0; i < ctx->n_outs; ++i) memcpy(ctx->outs[i].dst, ctx->outs[i].src, ctx->outs[i].bytes);
+  ctx->n_outs = 0;
+}
+
+// A pinned region of `bytes` for the current call.  When the call's regions no
+// longer fit, its queued work is waited for, the results staged so far are
+// delivered, and the buffer regrows.
+int pin_take(g4_ctx *ctx, size_t bytes, char **out) {
+  if (ctx->pin_used + up(bytes) > ctx->pin_bytes || ctx->n_outs == 8) {
+    G4_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    flush_outs(ctx);
+    ctx->pin_used = 0;
+    if (up(bytes) > ctx->pin_bytes) {
+      if (ctx->pin) G4_HIP(hipHostFree(ctx->pin), "hipHostFree");
+      ctx->pin = nullptr;
+      ctx->pin_bytes = 0;
+      size_t want = up(bytes) < (size_t(1) << 20) ? (size_t(1) << 20) : up(bytes);
+      void *p = nullptr;
+      G4_HIP(hipHostMalloc(&p, want, hipHostMallocDefault), "hipHostMalloc");
+      ctx->pin = (char *)p;
+      ctx->pin_bytes = want;
+    }
+  }
+  *out = ctx->pin + ctx->pin_used;
+  ctx->pin_used += up(bytes);
+  return G4_OK;
+}
+
 int copy_in(g4_ctx *ctx, void *dst, const void *src, size_t bytes) {
-  if (bytes) G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync(H2D)");
+  if (!bytes) return G4_OK;
+  if (bytes > PIN_MAX_COPY || (bytes & 3) || ((uintptr_t)dst & 15)) {
+    G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync(H2D)");
+    return G4_OK;
+  }
+  char *p = nullptr;
+  const int rc = pin_take(ctx, bytes, &p);
+  if (rc != G4_OK) return rc;
+  memcpy(p, src, bytes);
+  G4_HIP(g4::launch_copy(dst, p, bytes, ctx->stream), "copy in");
   return G4_OK;
 }
 
 int copy_out(g4_ctx *ctx, void *dst, const void *src, size_t bytes) {
-  if (bytes) G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync(D2H)");
+  if (!bytes) return G4_OK;
+  if (bytes > PIN_MAX_COPY || (bytes & 3) || ((uintptr_t)src & 15)) {
+    G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync(D2H)");
+    return G4_OK;
+  }
+  char *p = nullptr;
+  const int rc = pin_take(ctx, bytes, &p);
+  if (rc != G4_OK) return rc;
+  G4_HIP(g4::launch_copy(p, src, bytes, ctx->stream), "copy out");
+  ctx->outs[ctx->n_outs++] = G4PendingOut{dst, p, bytes};
   return G4_OK;
 }
 
+// Where a host-pointer call's kernels write a result meant for `dst`: a small
+// result straight into pinned host memory (the kernels store across the bus, no
+// copy launch) that reaches `dst` when the call ends; a larger one into
+// `fallback` in device memory, for copy_out.  *direct tells which.
+int stage_out(g4_ctx *ctx, void *dst, size_t bytes, void *fallback, void **dev, bool *direct) {
+  *dev = fallback;
+  *direct = false;
+  if (!bytes || bytes > PIN_MAX_COPY || (bytes & 3)) return G4_OK;
+  char *p = nullptr;
+  const int rc = pin_take(ctx, bytes, &p);
+  if (rc != G4_OK) return rc;
+  ctx->outs[ctx->n_outs++] = G4PendingOut{dst, p, bytes};
+  *dev = p;
+  *direct = true;
+  return G4_OK;
+}
+
+// End of a host-pointer call: wait, then hand the staged results to the caller.
 int finish(g4_ctx *ctx) {
   G4_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  flush_outs(ctx);
+  ctx->pin_used = 0;
   return G4_OK;
 }
 
@@ -583,6 +676,7 @@ int g4_close(g4_ctx *ctx) {
   (void)hipStreamSynchronize(ctx->own_stream);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->am_val) (void)hipFree(ctx->am_val);
+  if (ctx->pin) (void)hipHostFree(ctx->pin);
   (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
   return G4_OK;
@@ -681,10 +775,13 @@ int g4_matmul(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const float 
   Carve c;
   size_t ox = c.add(sizeof(float) * (size_t)dim1), oy = c.add(sizeof(float) * (size_t)dim0);
   G4_TRY(ensure_scratch(ctx, c.off));
-  float *dx = (float *)(ctx->scratch + ox), *dy = (float *)(ctx->scratch + oy);
+  float *dx = (float *)(ctx->scratch + ox);
+  void *dy = nullptr;
+  bool direct = false;
   G4_TRY(copy_in(ctx, dx, that, sizeof(float) * (size_t)dim1));
-  G4_TRY(matmul_dev(ctx, w, this_offset, dx, dy, dim0, dim1));
-  G4_TRY(copy_out(ctx, out, dy, sizeof(float) * (size_t)dim0));
+  G4_TRY(stage_out(ctx, out, sizeof(float) * (size_t)dim0, ctx->scratch + oy, &dy, &direct));
+  G4_TRY(matmul_dev(ctx, w, this_offset, dx, (float *)dy, dim0, dim1));
+  if (!direct) G4_TRY(copy_out(ctx, out, dy, sizeof(float) * (size_t)dim0));
   return finish(ctx);
 }
 

@@ -1177,6 +1177,29 @@ hipError_t launch_moe_down(int type, const RowsArgs &a, const float *gw, int32_t
   }
 }
 
+// dst[0 .. bytes) = src[0 .. bytes): bytes a multiple of 4, both ends 16-byte
+// aligned.  Moves the host-pointer entry points' activations between pinned host
+// memory and the device without a DMA command (the copy engines' start-up cost
+// more than these few kilobytes).
+__global__ __launch_bounds__(256) void k_copy(uint32_t *dst, const uint32_t *src, int64_t words) {
+  const int64_t n4 = words >> 2;
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += step)
+    ((u32x4 *)dst)[i] = ((const u32x4 *)src)[i];
+  for (int64_t i = 4 * n4 + blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < words; i += step) dst[i] = src[i];
+}
+
+hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return hipSuccess;
+  if ((bytes & 3) || ((uintptr_t)dst & 15) || ((uintptr_t)src & 15)) return hipErrorInvalidValue;
+  const int64_t words = (int64_t)(bytes >> 2);
+  int64_t blocks = (words / 4 + 255) / 256;
+  if (blocks > 256) blocks = 256;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(k_copy, dim3((unsigned)blocks), dim3(256), 0, s, (uint32_t *)dst, (const uint32_t *)src, words);
+  return hipGetLastError();
+}
+
 hipError_t launch_moe_combine(const float *ys, const float *weights, int32_t T, int32_t k, int32_t dim, float *Y,
                               hipStream_t s) {
   const int64_t n = (int64_t)T * dim;
