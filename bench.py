@@ -50,18 +50,18 @@ Q8_0, Q4_0, Q4_K = 8, 2, 12
 # (KiB), the factors being what the counters read for a plain 256 MiB fp32 copy.
 # Recorded in profiles/hbm_traffic_fetch_write_size.md (same command and kernels).
 TRAFFIC_BYTES = {
-    "q4_0_ffn_decode_token": 19173171,
-    "q8_0_matvec_2048x2048": 4633395,
-    "q8_0_lm_head_262144x2048_argmax": 572318720,
-    "q4_k_batched_8192x2048_m1": 9641779,
+    "q4_0_ffn_decode_token": 19200819,
+    "q8_0_matvec_2048x2048": 4625203,
+    "q8_0_lm_head_262144x2048_argmax": 572274893,
+    "q4_k_batched_8192x2048_m1": 9654067,
     "q4_k_batched_8192x2048_m8": 10430259,
     "q4_k_batched_8192x2048_m32": 16970547,
     "q4_k_batched_8192x2048_m64": 32674611,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40324301,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 554032538,
-    "q5_k_matvec_8192x2048": 11775795,
-    "q6_k_matvec_8192x2048": 14026547,
-    "q4_0_ffn_block_decode_token": 29163110,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40342733,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 553566362,
+    "q5_k_matvec_8192x2048": 11759411,
+    "q6_k_matvec_8192x2048": 14134067,
+    "q4_0_ffn_block_decode_token": 29185638,
     "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572318003,
     "attention_decode_h16_kv8_d256_len8192": 136787149,
 }
