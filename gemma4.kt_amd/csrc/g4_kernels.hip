@@ -283,7 +283,7 @@ G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *
 
 // --------------------------------------------------------------- engine ----
 
-template <class F, int LPR, int CPL, int EPI, bool MULTI, bool NORM, bool ROUTE = false>
+template <class F, int LPR, int CPL, int EPI, bool MULTI, bool NORM, bool ROUTE = false, bool XL = false>
 __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1;  // row steps per tile (about F::RT chunk loads per lane)
   constexpr int RPW = 64 / LPR;                  // rows in flight per step (one per lane group)
@@ -291,13 +291,27 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   constexpr int LRT = (EPI == EPI_GELU_PAIR) ? TR / 2 : TR;  // logical rows per tile
   constexpr int NDW = F::NDW;
   constexpr int NCH = LPR * CPL;                 // x chunks of one column pass
-  constexpr int XSEG = NCH * 16 / 256;           // 16-byte x segments each of the 256 threads stages
+  constexpr int XSEG = (NCH * 16 + 255) / 256;   // 16-byte x segments each of the 256 threads stages
+  constexpr bool XFULL = NCH * 16 % 256 == 0;     // every thread's last segment is one of the pass's
   static_assert(RT >= 1, "tile");
   static_assert(EPI != EPI_GELU_PAIR || (RT >= 2 && CPL == 1), "paired tiles: gate and up steps, one pass");
-  static_assert(XSEG >= 1 && XSEG * 256 == NCH * 16, "x staging");
+  static_assert(XSEG >= 1 && (XFULL || (!NORM && !MULTI)), "x staging");
   static_assert(!(NORM && MULTI), "the fused norm needs all of x in one pass");
   static_assert(!ROUTE || (EPI == EPI_GELU_PAIR && !MULTI && !NORM), "routing: gate+up launches");
-  __shared__ u32x4 xl[NCH * 16];
+  // XL: each chunk's x is read from LDS when its weights are dotted instead of
+  // living in VGPRs for the whole launch, so a lane can take CPL = 3 chunks
+  // (rows of 17..24 chunks, e.g. 1408 columns, keep 22 of 24 lanes busy rather
+  // than 22 of 32); the block sums of x are computed once into LDS
+  static_assert(!XL || (EPI == EPI_STORE && !MULTI && !NORM && !ROUTE), "x at use: plain single-pass launches");
+  constexpr int NSX = F::NS > 0 ? F::NS : 1;
+  // x layout in LDS (16-byte slots): chunk ch's segment i sits at slot
+  // ch * 16 + (i ^ (ch & 15)) -- the 8 lanes one LDS cycle serves read 8
+  // different bank groups; with XL at ch * 17 + i instead (the same spread, and
+  // the 16 reads of a chunk share one address register and immediate offsets)
+  constexpr int XCS = XL ? 17 : 16;
+  auto xslot = [](int ch, int i) { return XL ? ch * 17 + i : ch * 16 + (i ^ (ch & 15)); };
+  __shared__ u32x4 xl[NCH * XCS];
+  __shared__ float xsl[XL ? NCH : 1][NSX];
   __shared__ float red[4];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -422,15 +436,41 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     aq_n = 0;
   };
 
+  auto read_x = [&](int ch, float (&xu)[64]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const u32x4 t = xl[xslot(ch, i)];
+      xu[4 * i] = __uint_as_float(t.x);
+      xu[4 * i + 1] = __uint_as_float(t.y);
+      xu[4 * i + 2] = __uint_as_float(t.z);
+      xu[4 * i + 3] = __uint_as_float(t.w);
+    }
+  };
+  constexpr int CX = XL ? 1 : CPL;  // chunks of x held in VGPRs
   auto finish_tile = [&](int t, int pass, const uint32_t (&D)[RT][CPL][NDW], const bool (&ok)[RT][CPL],
-                         const int64_t (&E)[RT][CPL], const float (&xv)[CPL][64], const float (&xs)[CPL][F::NS > 0 ? F::NS : 1]) {
+                         const int64_t (&E)[RT][CPL], const float (&xv)[CX][64], const float (&xs)[CX][NSX]) {
     float v[RT];
 #pragma unroll
     for (int k = 0; k < RT; ++k) {
       float acc = 0.f;
 #pragma unroll
       for (int u = 0; u < CPL; ++u) {
-        const float r = F::dot(D[k][u], xv[u], xs[u], E[k][u]);
+        float r;
+        if constexpr (XL) {
+          float xu[64], su[NSX];
+          // an opaque chunk index: the reads are the same for every tile, and
+          // hoisting them out of the tile loop would hold every chunk's x in VGPRs
+          const int ch = (int)opaque((uint32_t)(u * LPR + q));
+          read_x(ch, xu);
+#pragma unroll
+          for (int j = 0; j < NSX; ++j) su[j] = xsl[ch][j];
+          r = F::dot(D[k][u], xu, su, E[k][u]);
+          // one chunk's x in VGPRs at a time: this chunk's dot is done before
+          // the next chunk's LDS reads are issued
+          asm volatile("" : "+v"(r)::"memory");
+        } else {
+          r = F::dot(D[k][u], xv[u], xs[u], E[k][u]);
+        }
         acc += ok[k][u] ? r : 0.f;
       }
       v[k] = acc;
@@ -511,27 +551,29 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
       // zeroed by a mask, not a select: a select lets the compiler sink the
       // load into a branch, whose wait would then cover the weight loads too
       const uint32_t m = opaque(c < C ? ~0u : 0u);
-      xl[ch * 16 + ((s & 15) ^ (ch & 15))] = u32x4{xr[j].x & m, xr[j].y & m, xr[j].z & m, xr[j].w & m};
+      if (XFULL || ch < NCH) xl[xslot(ch, s & 15)] = u32x4{xr[j].x & m, xr[j].y & m, xr[j].z & m, xr[j].w & m};
     }
     __syncthreads();
-    // chunk ch's 16-byte segment i sits at slot i ^ (ch & 15): the 8 lanes one
-    // LDS cycle serves read 8 different bank groups
-    float xv[CPL][64];
+    float xv[CX][64];
+    float xs[CX][NSX];
+    if constexpr (XL) {
+      if constexpr (F::NS > 0) {
+        // one thread per chunk (NCH <= 256) sums its blocks once for the workgroup
+        if (tid < NCH) {
+          float xu[64], su[NSX];
+          read_x(tid, xu);
+          F::sums(xu, su);
 #pragma unroll
-    for (int u = 0; u < CPL; ++u) {
-      const int ch = u * LPR + q;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const u32x4 t = xl[ch * 16 + (i ^ (ch & 15))];
-        xv[u][4 * i] = __uint_as_float(t.x);
-        xv[u][4 * i + 1] = __uint_as_float(t.y);
-        xv[u][4 * i + 2] = __uint_as_float(t.z);
-        xv[u][4 * i + 3] = __uint_as_float(t.w);
+          for (int j = 0; j < NSX; ++j) xsl[tid][j] = su[j];
+        }
+        __syncthreads();
       }
-    }
-    float xs[CPL][F::NS > 0 ? F::NS : 1];
+    } else {
 #pragma unroll
-    for (int u = 0; u < CPL; ++u) F::sums(xv[u], xs[u]);
+      for (int u = 0; u < CPL; ++u) read_x(u * LPR + q, xv[u]);
+#pragma unroll
+      for (int u = 0; u < CPL; ++u) F::sums(xv[u], xs[u]);
+    }
 
     // software pipeline: tile t+1 is in flight while tile t is unpacked and
     // reduced (only the first tile goes out with x: issuing the second one too
@@ -894,7 +936,7 @@ struct OneStep : F {
   static constexpr int RT = 1;
 };
 
-template <class F, int LPR, int CPL>
+template <class F, int LPR, int CPL, bool XL = false>
 static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, const DevInfo &dev, hipStream_t s) {
   constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1, RPW = 64 / LPR, TR = RT * RPW;
   typedef void (*Kernel)(RowsArgs);
@@ -904,7 +946,9 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
   if (norm && (multi || segments != 1)) return hipErrorInvalidValue;
   if (route && (epi != EPI_GELU_PAIR || multi)) return hipErrorInvalidValue;
   Kernel k = nullptr;
-  if (epi == EPI_STORE) {
+  if constexpr (XL) {
+    if (epi == EPI_STORE && !norm && !route && !multi) k = k_rows<F, LPR, CPL, EPI_STORE, false, false, false, true>;
+  } else if (epi == EPI_STORE) {
     k = norm ? k_rows<F, LPR, CPL, EPI_STORE, false, true> : k_rows<F, LPR, CPL, EPI_STORE, false, false>;
     if constexpr (LPR == 64 && CPL == 2)
       if (multi) k = k_rows<F, LPR, CPL, EPI_STORE, true, false>;
@@ -980,6 +1024,13 @@ static hipError_t launch_fast(int epi, const RowsArgs &a, int segments, const De
     }
   }
   if (C > 32) return launch_fast_cfg<F, 64, 1>(epi, a, segments, dev, s);
+  // rows of 17..24 chunks (the MoE down projection's 1408 columns are 22): 8
+  // lanes x 3 chunks with x read at use keep 22 of 24 lanes busy, against 22 of
+  // 32 with one chunk per lane (16 tokens of 128-expert top-8 MoE: 127 -> 117 us
+  // per step); for the formats whose three chunk buffers fit the VGPRs
+  if constexpr (F::NDW <= 20)
+    if (C > 16 && C <= 24 && epi == EPI_STORE && !a.norm_w)
+      return launch_fast_cfg<F, 8, 3, true>(epi, a, segments, dev, s);
   if (C > 16) return launch_fast_cfg<F, 32, 1>(epi, a, segments, dev, s);
   return launch_fast_cfg<F, 16, 1>(epi, a, segments, dev, s);
 }

@@ -130,6 +130,15 @@ def lib(path: Optional[str] = None) -> ctypes.CDLL:
     path = path or LIB_PATH
     if not os.path.exists(path):
         raise OSError("libg4hip.so not found at %s: run gemma4.kt_amd/build.py (no CPU fallback exists)" % path)
+    # The *_dev wrappers take torch's device tensors and streams, so the library
+    # must run on torch's HIP runtime.  torch ships its own libamdhip64 and puts
+    # it in the process's global symbol scope when imported; a library loaded
+    # before torch binds its HIP calls to the system runtime instead, leaving two
+    # runtimes in one process whose stream handles and queues are not shared.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = ctypes.CDLL(path)
     for name, argtypes in SIGNATURES.items():
         fn = getattr(L, name)

@@ -84,6 +84,7 @@ SHAPES = [
     (37, 1024, 3, "aligned 1024, odd rows, row offset"),
     (19, 8192, 1, "multi-pass 8192"),
     (24, 1408, 1, "1408 (Q4_K rows straddle super-blocks)"),
+    (13, 1536, 2, "1536 (24 chunks, x read at use)"),
     (9, 640, 0, "short rows (16-lane groups)"),
 ]
 
@@ -105,6 +106,22 @@ def test_matmul_fast_path(g4, ctx, oracle, t, shape):
     assert_dots(y, ex, ab, "type %d %r" % (t, shape))
     ref = oracle.matmul(t, raw, x, dim0, dim1, off)
     assert_dots(ref, ex, ab, "oracle")
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q5_K])
+def test_matmul_x_at_use_many_tiles(g4, ctx, oracle, t):
+    """17 chunks per row (8 lanes x 3 chunks, x read from LDS per chunk), with
+    enough rows that every wave runs three tiles and the last one is partial."""
+    dim0, dim1 = 36001, 1088
+    announce("matmul x-at-use type=%d %dx%d" % (t, dim0, dim1))
+    n = (dim0 * dim1 + 255) // 256 * 256
+    raw = synth.weights(44, "xl%d" % t, t, n)
+    x = synth.activations(44, "xl", dim1)
+    w = upload(g4, ctx, t, raw, n)
+    y = np.empty(dim0, np.float32)
+    w.matmul(x, y, dim0, dim1, 0)
+    ex, ab = oracle.matmul_exact(t, raw, x, dim0, dim1, 0)
+    assert_dots(y, ex, ab, "x at use type %d" % t)
 
 
 GENERIC = [(5, 1000, 7), (3, 33, 1), (4, 2048, 32), (2, 96, 64 + 32), (6, 17, 0), (1, 5, 250)]
