@@ -57,8 +57,8 @@ TRAFFIC_BYTES = {
     "q4_k_batched_8192x2048_m8": 10430259,
     "q4_k_batched_8192x2048_m32": 16970547,
     "q4_k_batched_8192x2048_m64": 32674611,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40342733,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 553566362,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40358195,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 547822899,
     "q5_k_matvec_8192x2048": 11759411,
     "q6_k_matvec_8192x2048": 14134067,
     "q4_0_ffn_block_decode_token": 29185638,

@@ -768,7 +768,10 @@ __global__ __launch_bounds__(256) void k_moe_down(RowsArgs a, const float *gw, i
   uint32_t DA[RT][NDW], DB[RT][NDW];
   bool okA[RT], okB[RT];
   int64_t EA[RT], EB[RT];
+  // both slots' weights go out before the x staging waits (one token's step:
+  // 21.6 -> 21.3 us against issuing the second slot after the barrier)
   load(wid, DA, okA, EA);
+  load(wid + 4, DB, okB, EB);
 #pragma unroll
   for (int u = 0; u < XSEG; ++u) {
     const int g = u * 256 + tid, j = g / XS, c = (g % XS) >> 4;
@@ -776,7 +779,6 @@ __global__ __launch_bounds__(256) void k_moe_down(RowsArgs a, const float *gw, i
     xl[j][c * 16 + ((g & 15) ^ (c & 15))] = u32x4{xr[u].x & m, xr[u].y & m, xr[u].z & m, xr[u].w & m};
   }
   __syncthreads();
-  load(wid + 4, DB, okB, EB);
   __builtin_amdgcn_sched_barrier(0);
   if (wid < K) finish(wid, DA, okA, EA);
   __builtin_amdgcn_sched_barrier(0);
