@@ -37,6 +37,21 @@ def test_library_exports_every_header_symbol(g4):
     assert set(g4.SIGNATURES) == set(header_symbols())
 
 
+def test_library_binds_to_torchs_hip_runtime():
+    """Loaded through g4hip in a fresh interpreter, the library's HIP calls resolve
+    to torch's own libamdhip64 (the runtime torch's tensors and streams live in),
+    not to a second runtime from the system path."""
+    code = ("import sys; sys.path.insert(0, %r); import g4hip; g4hip.lib(); "
+            "assert 'torch' in sys.modules" % os.path.join(ROOT, "gemma4.kt_amd"))
+    env = dict(os.environ, LD_DEBUG="bindings")
+    r = subprocess.run(["python3", "-c", code], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, env=env,
+                       timeout=600)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [l for l in r.stderr.splitlines() if "libg4hip.so" in l and "`hipLaunchKernel'" in l]
+    assert lines, "no binding record for hipLaunchKernel"
+    assert all("torch/lib/libamdhip64" in l for l in lines), lines
+
+
 def test_no_device_here(g4):
     assert g4.device_count() == 0
     with pytest.raises(g4.IllegalStateException):
