@@ -39,10 +39,11 @@ static_assert(NORM_WEIGHT_AFTER == G4_NORM_WEIGHT_AFTER && NORM_WEIGHT_FIRST == 
 // 1 MB of freshly written logits.  So each block stores its partial with a plain
 // store and k_argmax_final (one block) reduces them after the kernel boundary.
 
-// (value, index) of the block in thread 0 (all threads call, uniform control flow).
+// (value, index) of the block in thread 0 (all threads call, uniform control
+// flow; blocks of up to 16 waves).
 __device__ void am_block(float &v, int &i) {
-  __shared__ float rv[4];
-  __shared__ int ri[4];
+  __shared__ float rv[16];
+  __shared__ int ri[16];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, wpb = blockDim.x >> 6;
   am_wave(v, i);
   __syncthreads();
@@ -283,20 +284,23 @@ G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *
 
 // --------------------------------------------------------------- engine ----
 
-template <class F, int LPR, int CPL, int EPI, bool MULTI, bool NORM, bool ROUTE = false, bool XL = false>
-__global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
+template <class F, int LPR, int CPL, int EPI, bool MULTI, bool NORM, bool ROUTE = false, bool XL = false, int WPB = 4>
+__global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
+  constexpr int NT = 64 * WPB;                   // threads per workgroup (WPB waves)
   constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1;  // row steps per tile (about F::RT chunk loads per lane)
   constexpr int RPW = 64 / LPR;                  // rows in flight per step (one per lane group)
   constexpr int TR = RT * RPW;                   // physical rows per tile
   constexpr int LRT = (EPI == EPI_GELU_PAIR) ? TR / 2 : TR;  // logical rows per tile
   constexpr int NDW = F::NDW;
   constexpr int NCH = LPR * CPL;                 // x chunks of one column pass
-  constexpr int XSEG = (NCH * 16 + 255) / 256;   // 16-byte x segments each of the 256 threads stages
-  constexpr bool XFULL = NCH * 16 % 256 == 0;     // every thread's last segment is one of the pass's
+  constexpr int XSEG = (NCH * 16 + NT - 1) / NT;  // 16-byte x segments each thread stages
+  constexpr bool XFULL = NCH * 16 % NT == 0;      // every thread's last segment is one of the pass's
   static_assert(RT >= 1, "tile");
   static_assert(EPI != EPI_GELU_PAIR || (RT >= 2 && CPL == 1), "paired tiles: gate and up steps, one pass");
   static_assert(XSEG >= 1 && (XFULL || (!NORM && !MULTI)), "x staging");
   static_assert(!(NORM && MULTI), "the fused norm needs all of x in one pass");
+  static_assert(!NORM || WPB == 4, "the fused norm uses the 256-thread element map of k_rmsnorm");
+  static_assert(WPB == 4 || WPB == 8, "workgroup of 4 or 8 waves");
   static_assert(!ROUTE || (EPI == EPI_GELU_PAIR && !MULTI && !NORM), "routing: gate+up launches");
   // XL: each chunk's x is read from LDS when its weights are dotted instead of
   // living in VGPRs for the whole launch, so a lane can take CPL = 3 chunks
@@ -316,7 +320,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: tile loop control stays scalar
-  constexpr int wpb = 4;                         // launched with 256 threads
+  constexpr int wpb = WPB;
   const int gi = lane / LPR, q = lane % LPR;
   const int seg = blockIdx.y;
   const int C = a.dim1 >> 6;
@@ -328,7 +332,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   auto load_x = [&](int pass) {
 #pragma unroll
     for (int j = 0; j < XSEG; ++j) {
-      const int s = j * 256 + tid, c = pass * NCH + (s >> 4);
+      const int s = j * NT + tid, c = pass * NCH + (s >> 4);
       // dword alignment is all a caller's x guarantees; gfx950 takes 128-bit loads at that alignment
       xr[j] = ((const u32x4a4 *)(x + (int64_t)(c < C ? c : 0) * 64))[s & 15];
       if constexpr (NORM) wr[j] = ((const u32x4a4 *)(a.norm_w + (int64_t)(c < C ? c : 0) * 64))[s & 15];
@@ -403,7 +407,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   // LDS queue, and gelu (in double, like the reference) runs once per 64 rows
   // with every lane busy rather than once per tile with one lane per row.  The
   // queued rows are contiguous because a wave finishes its tiles in order.
-  __shared__ float2 gq[EPI == EPI_GELU_PAIR ? 4 : 1][64];
+  __shared__ float2 gq[EPI == EPI_GELU_PAIR ? WPB : 1][64];
   int gq_n = 0, gq_row = t0 * LRT;
   auto gq_flush = [&]() {
     if (lane < gq_n) {
@@ -419,7 +423,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   // soft-cap's double tanh, the store and the arg-max update run once per 64
   // rows with every lane busy (coalesced stores), not once per tile.
   constexpr bool AQ = EPI == EPI_ARGMAX && !MULTI;
-  __shared__ float aq[AQ ? 4 : 1][64];
+  __shared__ float aq[AQ ? WPB : 1][64];
   int aq_n = 0, aq_row = t0 * LRT;
   auto aq_flush = [&]() {
     if (lane < aq_n) {
@@ -547,7 +551,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < XSEG; ++j) {
-      const int s = j * 256 + tid, ch = s >> 4, c = pass * NCH + ch;
+      const int s = j * NT + tid, ch = s >> 4, c = pass * NCH + ch;
       // zeroed by a mask, not a select: a select lets the compiler sink the
       // load into a branch, whose wait would then cover the weight loads too
       const uint32_t m = opaque(c < C ? ~0u : 0u);
@@ -596,10 +600,12 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     // The rows still queued when the tiles run out: when the four waves' rows
     // fit in 64 lanes, one wave evaluates them all (one double-precision gelu
     // pass per workgroup instead of one per wave at the kernel's tail).
-    __shared__ int gq_meta[4][2];
+    __shared__ int gq_meta[WPB][2];
     if (lane == 0) gq_meta[wid][0] = gq_n, gq_meta[wid][1] = gq_row;
     __syncthreads();
-    const int tot = gq_meta[0][0] + gq_meta[1][0] + gq_meta[2][0] + gq_meta[3][0];
+    int tot = 0;
+#pragma unroll
+    for (int w = 0; w < WPB; ++w) tot += gq_meta[w][0];
     if (tot <= 64) {
       if (wid == 0 && lane < tot) {
         int w = 0, k = lane;
@@ -938,18 +944,30 @@ struct OneStep : F {
   static constexpr int RT = 1;
 };
 
-template <class F, int LPR, int CPL, bool XL = false>
+template <class F, int LPR, int CPL, bool XL = false, int WPB = 4>
 static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, const DevInfo &dev, hipStream_t s) {
   constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1, RPW = 64 / LPR, TR = RT * RPW;
   typedef void (*Kernel)(RowsArgs);
   const bool multi = (a.dim1 / 64) > LPR * CPL;
   const bool norm = a.norm_w != nullptr;
   const bool route = a.route_logits != nullptr;
+  // the fused norm and the routing prologue use 256-thread reductions
+  if constexpr (WPB != 4)
+    if (norm || route) return launch_fast_cfg<F, LPR, CPL, XL, 4>(epi, a, segments, dev, s);
   if (norm && (multi || segments != 1)) return hipErrorInvalidValue;
   if (route && (epi != EPI_GELU_PAIR || multi)) return hipErrorInvalidValue;
   Kernel k = nullptr;
   if constexpr (XL) {
-    if (epi == EPI_STORE && !norm && !route && !multi) k = k_rows<F, LPR, CPL, EPI_STORE, false, false, false, true>;
+    if (epi == EPI_STORE && !norm && !route && !multi)
+      k = k_rows<F, LPR, CPL, EPI_STORE, false, false, false, true, WPB>;
+  } else if constexpr (WPB != 4) {
+    if (epi == EPI_STORE) k = k_rows<F, LPR, CPL, EPI_STORE, false, false, false, false, WPB>;
+    else if (epi == EPI_ARGMAX) k = k_rows<F, LPR, CPL, EPI_ARGMAX, false, false, false, false, WPB>;
+    else if constexpr (CPL == 1 && F::RT >= 2) k = k_rows<F, LPR, 1, EPI_GELU_PAIR, false, false, false, false, WPB>;
+    if constexpr (LPR == 64 && CPL == 2) {
+      if (multi && epi == EPI_STORE) k = k_rows<F, LPR, CPL, EPI_STORE, true, false, false, false, WPB>;
+      if (multi && epi == EPI_ARGMAX) k = k_rows<F, LPR, CPL, EPI_ARGMAX, true, false, false, false, WPB>;
+    }
   } else if (epi == EPI_STORE) {
     k = norm ? k_rows<F, LPR, CPL, EPI_STORE, false, true> : k_rows<F, LPR, CPL, EPI_STORE, false, false>;
     if constexpr (LPR == 64 && CPL == 2)
@@ -976,7 +994,7 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
   int res = slot.load(std::memory_order_relaxed);
   if (res == 0) {
     int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 256, 0) != hipSuccess || nb < 1) nb = 2;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 64 * WPB, 0) != hipSuccess || nb < 1) nb = 8 / WPB;
     res = nb;
     slot.store(res, std::memory_order_relaxed);
   }
@@ -984,22 +1002,23 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
   const int64_t n_tiles = (a.rows + lrt - 1) / lrt;
   const int64_t segs = segments > 0 ? segments : 1;
   const int64_t cu = dev.cu_count;
-  // 4-wave workgroups sharing one LDS copy of x.  About two tiles per wave (one
-  // computing while the next is in flight), rounded up to whole rounds of one
-  // workgroup per CU over all segments (a partial round leaves CUs with half
-  // the work of the others), at most what is resident at once, never more
+  // WPB-wave workgroups sharing one LDS copy of x.  About two tiles per wave
+  // (one computing while the next is in flight), rounded up to whole rounds of
+  // one workgroup per CU over all segments (a partial round leaves CUs with
+  // half the work of the others), at most what is resident at once, never more
   // workgroups than tiles (idle waves only help stage x).
-  int64_t blocks = (n_tiles + 4 * G4_TILES_PER_WAVE - 1) / (4 * G4_TILES_PER_WAVE);
+  int64_t blocks = (n_tiles + WPB * G4_TILES_PER_WAVE - 1) / (WPB * G4_TILES_PER_WAVE);
   blocks = ((blocks * segs + cu - 1) / cu * cu + segs - 1) / segs;
-  // at most two resident workgroups per CU: with more requests in flight a long
+  // at most eight resident waves per CU: with more requests in flight a long
   // stream (the 570 MB LM head) was measured slower, and the small launches
   // never reach the cap
-  const int64_t cap = cu * (res < 2 ? res : 2) / segs;
+  constexpr int WG_CAP = 8 / WPB;
+  const int64_t cap = cu * (res < WG_CAP ? res : WG_CAP) / segs;
   if (blocks > cap) blocks = cap;
   if (blocks > n_tiles) blocks = n_tiles;
   if (blocks < 1) blocks = 1;
   if (epi == EPI_ARGMAX && blocks > max_argmax_blocks(dev)) blocks = max_argmax_blocks(dev);
-  hipLaunchKernelGGL(k, dim3((unsigned)blocks, (unsigned)segments), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k, dim3((unsigned)blocks, (unsigned)segments), dim3(64 * WPB), 0, s, a);
   if (epi == EPI_ARGMAX) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1024,6 +1043,14 @@ static hipError_t launch_fast(int epi, const RowsArgs &a, int segments, const De
       if (C > 16) return launch_fast_cfg<OneStep<F>, 32, 1>(epi, a, segments, dev, s);
       return launch_fast_cfg<OneStep<F>, 16, 1>(epi, a, segments, dev, s);
     }
+  }
+  // The arg-max matvec over a vocabulary (no fused norm) takes one 8-wave
+  // workgroup per CU instead of two 4-wave ones: the 262144-row Q8_0 LM head
+  // measured 100.3 -> 98.9 us (the small matvecs lost 0.5-1 us that way)
+  if (epi == EPI_ARGMAX && !a.norm_w && (int64_t)a.rows * segments >= 65536) {
+    if (C > 32) return launch_fast_cfg<F, 64, 1, false, 8>(epi, a, segments, dev, s);
+    if (C > 16) return launch_fast_cfg<F, 32, 1, false, 8>(epi, a, segments, dev, s);
+    return launch_fast_cfg<F, 16, 1, false, 8>(epi, a, segments, dev, s);
   }
   if (C > 32) return launch_fast_cfg<F, 64, 1>(epi, a, segments, dev, s);
   // rows of 17..24 chunks (the MoE down projection's 1408 columns are 22): 8

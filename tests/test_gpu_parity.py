@@ -346,6 +346,41 @@ def test_q8_0_lm_head_argmax(g4, ctx, oracle):
     assert w.matmul_argmax(c["x"], V, D) == idx
 
 
+def test_matmul_argmax_winner_in_every_wave(g4, ctx, oracle):
+    """A vocabulary-sized arg-max launch (65536 rows: one 8-wave workgroup per CU,
+    each wave a contiguous range of 32 rows, wave w of every workgroup covering
+    rows 8192 w .. 8192 w + 8191).  x is made equal to row 8192 w + 5, so that row
+    wins, for each w; then a copy of the winner at a lower row in another wave (same
+    position in its tile, so the two dots are bit-equal) must win the tie."""
+    V, D = 65536, 1088
+    announce("matmul_argmax 8-wave groups %dx%d" % (V, D))
+    n = V * D
+    raw = synth.weights(61, "am8", Q8_0, n)
+    w = upload(g4, ctx, Q8_0, raw, n)
+    for wave in range(8):
+        r = 8192 * wave + 5
+        x = oracle.dequant(Q8_0, raw, r * D, D)
+        logits = np.empty(V, np.float32)
+        idx = w.matmul_argmax(x, V, D, logits=logits)
+        ex, ab = oracle.matmul_exact(Q8_0, raw, x, V, D)
+        assert_dots(logits, ex, ab, "argmax wave %d" % wave)
+        order = np.argsort(-ex, kind="stable")
+        assert int(order[0]) == r, "fixture: row %d is not the exact winner" % r
+        assert ex[order[0]] - ex[order[1]] > 2 * TOL * max(ab[order[0]], ab[order[1]])
+        assert idx == r, (wave, idx)
+    # tie across waves: row 8192 * 2 + 5 becomes a copy of row 8192 * 6 + 5
+    bpr = D // 32 * 34
+    tied = np.array(raw, dtype=np.uint8, copy=True)
+    win, low = 8192 * 6 + 5, 8192 * 2 + 5
+    tied[low * bpr:(low + 1) * bpr] = tied[win * bpr:(win + 1) * bpr]
+    wt = upload(g4, ctx, Q8_0, tied, n)
+    x = oracle.dequant(Q8_0, tied, win * D, D)
+    logits = np.empty(V, np.float32)
+    idx = wt.matmul_argmax(x, V, D, logits=logits)
+    assert logits[low] == logits[win]
+    assert idx == low == oracle.argmax(logits)
+
+
 @pytest.mark.parametrize("m", [1, 8, 32, 64])
 def test_q4_k_batched(g4, ctx, oracle, m):
     announce("workload q4_k batched M=%d" % m)
