@@ -52,7 +52,7 @@ Q8_0, Q4_0, Q4_K = 8, 2, 12
 TRAFFIC_BYTES = {
     "q4_0_ffn_decode_token": 19200819,
     "q8_0_matvec_2048x2048": 4625203,
-    "q8_0_lm_head_262144x2048_argmax": 572274893,
+    "q8_0_lm_head_262144x2048_argmax": 572074394,
     "q4_k_batched_8192x2048_m1": 9654067,
     "q4_k_batched_8192x2048_m8": 10430259,
     "q4_k_batched_8192x2048_m32": 16970547,
