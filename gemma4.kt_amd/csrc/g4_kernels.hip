@@ -1047,7 +1047,7 @@ static hipError_t launch_fast(int epi, const RowsArgs &a, int segments, const De
   // The arg-max matvec over a vocabulary (no fused norm) takes one 8-wave
   // workgroup per CU instead of two 4-wave ones: the 262144-row Q8_0 LM head
   // measured 100.3 -> 98.9 us (the small matvecs lost 0.5-1 us that way)
-  if (epi == EPI_ARGMAX && !a.norm_w && (int64_t)a.rows * segments >= 65536) {
+  if (epi == EPI_ARGMAX && !a.norm_w && (int64_t)a.rows * segments >= 65536 && C <= 64) {
     if (C > 32) return launch_fast_cfg<F, 64, 1, false, 8>(epi, a, segments, dev, s);
     if (C > 16) return launch_fast_cfg<F, 32, 1, false, 8>(epi, a, segments, dev, s);
     return launch_fast_cfg<F, 16, 1, false, 8>(epi, a, segments, dev, s);

@@ -346,16 +346,18 @@ def test_q8_0_lm_head_argmax(g4, ctx, oracle):
     assert w.matmul_argmax(c["x"], V, D) == idx
 
 
-def test_matmul_argmax_winner_in_every_wave(g4, ctx, oracle):
-    """A vocabulary-sized arg-max launch (65536 rows: one 8-wave workgroup per CU,
-    each wave a contiguous range of 32 rows, wave w of every workgroup covering
-    rows 8192 w .. 8192 w + 8191).  x is made equal to row 8192 w + 5, so that row
+@pytest.mark.parametrize("D", [1088, 2112, 640])
+def test_matmul_argmax_winner_in_every_wave(g4, ctx, oracle, D):
+    """A vocabulary-sized arg-max launch (65536 rows: one 8-wave workgroup per CU;
+    with 1088 columns each wave takes a contiguous range of 32 rows, wave w of every
+    workgroup covering rows 8192 w .. 8192 w + 8191; 2112 and 640 columns take the
+    64- and 16-lane row groups).  x is made equal to row 8192 w + 5, so that row
     wins, for each w; then a copy of the winner at a lower row in another wave (same
     position in its tile, so the two dots are bit-equal) must win the tie."""
-    V, D = 65536, 1088
+    V = 65536
     announce("matmul_argmax 8-wave groups %dx%d" % (V, D))
     n = V * D
-    raw = synth.weights(61, "am8", Q8_0, n)
+    raw = synth.weights(61, "am8.%d" % D, Q8_0, n)
     w = upload(g4, ctx, Q8_0, raw, n)
     for wave in range(8):
         r = 8192 * wave + 5
