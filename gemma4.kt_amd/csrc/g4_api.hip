@@ -251,7 +251,10 @@ int copy_out(g4_ctx *ctx, void *dst, const void *src, size_t bytes) {
 // Where a host-pointer call's kernels write a result meant for `dst`: a small
 // result straight into pinned host memory (the kernels store across the bus, no
 // copy launch) that reaches `dst` when the call ends; a larger one into
-// `fallback` in device memory, for copy_out.  *direct tells which.
+// `fallback` in device memory, for copy_out.  *direct tells which.  A call
+// stages its inputs first and its direct outputs last, right before the kernels
+// that write them: a later pin_take could otherwise wait, deliver the region
+// before it is written and reuse it.
 int stage_out(g4_ctx *ctx, void *dst, size_t bytes, void *fallback, void **dev, bool *direct) {
   *dev = fallback;
   *direct = false;
