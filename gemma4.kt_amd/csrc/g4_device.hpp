@@ -345,8 +345,11 @@ struct FmtQ6_K {
     const int64_t sb = e >> 8;
     const int c = (int)((e >> 6) & 3), n = c >> 1, p = c & 1;
     const uint8_t *S = W + sb * 210;
-    const u32x4a4 *ql = (const u32x4a4 *)((uintptr_t)(S + 64 * n) & ~(uintptr_t)3);
-    const u32x4a4 *qh = (const u32x4a4 *)((uintptr_t)(S + 128 + 32 * n) & ~(uintptr_t)3);
+    // dword-aligned windows by pointer arithmetic on W (a pointer rebuilt from an
+    // integer loses its global address space and compiles to flat loads)
+    const uint8_t *qlb = S + 64 * n, *qhb = S + 128 + 32 * n;
+    const u32x4a4 *ql = (const u32x4a4 *)(qlb - ((uintptr_t)qlb & 3));
+    const u32x4a4 *qh = (const u32x4a4 *)(qhb - ((uintptr_t)qhb & 3));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       u32x4a4 t = ql[i];

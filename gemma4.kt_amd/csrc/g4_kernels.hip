@@ -1035,7 +1035,7 @@ static hipError_t launch_fast(int epi, const RowsArgs &a, int segments, const De
   if (C > 64 && epi != EPI_GELU_PAIR) return launch_fast_cfg<F, 64, 2>(epi, a, segments, dev, s);
   // Q8_0 and Q6_K (the formats with the widest chunks, 17 and 29 dwords) take
   // one row step per tile up to 16384 rows: measured 4.55 -> 4.30 us on the
-  // 2048-row Q8_0 matvec and 8.04 -> 7.31 us on the 8192-row Q6_K one, while
+  // 2048-row Q8_0 matvec and 7.4 -> 6.6 us on the 8192-row Q6_K one, while
   // Q4_K got slower and the 262144-row LM head lost 1.4 us with it
   if constexpr (F::RT >= 2 && (F::TYPE == T_Q8_0 || F::TYPE == T_Q6_K)) {
     if (epi == EPI_STORE && (int64_t)a.rows * segments <= 16384) {
