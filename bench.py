@@ -60,7 +60,7 @@ TRAFFIC_BYTES = {
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40358195,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 547822899,
     "q5_k_matvec_8192x2048": 11759411,
-    "q6_k_matvec_8192x2048": 14134067,
+    "q6_k_matvec_8192x2048": 14136115,
     "q4_0_ffn_block_decode_token": 29185638,
     "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572318003,
     "attention_decode_h16_kv8_d256_len8192": 136787149,
