@@ -299,12 +299,14 @@ struct FmtQ5_K {
   G4_DEV static float dot(const uint32_t (&D)[NDW], const float *x, const float *s, int64_t e) {
     const int g = (int)((e >> 6) & 3);
     const uint32_t lsh = 2u * (uint32_t)g, hsh = lsh + 1u;
+    // fifth bits (bit lsh / hsh of each qh byte) rotated onto bit 4 of the same byte
+    const uint32_t lrot = (lsh - 4u) & 31u, hrot = (hsh - 4u) & 31u;
     float lo = 0.f, hi = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t Q = D[i], H = D[8 + i];
-      const uint32_t l = opaque((Q & 0x0F0F0F0Fu) | (((H >> lsh) & 0x01010101u) << 4));
-      const uint32_t h = opaque(((Q >> 4) & 0x0F0F0F0Fu) | (((H >> hsh) & 0x01010101u) << 4));
+      const uint32_t l = opaque((Q & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(H, H, lrot) & 0x10101010u));
+      const uint32_t h = opaque(((Q >> 4) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(H, H, hrot) & 0x10101010u));
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         lo = __builtin_fmaf(x[4 * i + b], ubyte(l, b), lo);
@@ -380,14 +382,16 @@ struct FmtQ6_K {
     const uint32_t al = (uint32_t)((e >> 8) & 1) * 2u;  // 210 * sb mod 4
     const uint32_t p = (uint32_t)((e >> 6) & 1);
     const uint32_t ns = 4u * p, s0 = 4u * p, s1 = s0 + 2u;
+    // bit pairs s0 / s1 of each qh byte rotated onto bits 4..5 of the same byte
+    const uint32_t r0 = (s0 - 4u) & 31u, r1 = (s1 - 4u) & 31u;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t qa = __builtin_amdgcn_alignbyte(D[i + 1], D[i], al);           // ql[l], l = 4i..4i+3
       const uint32_t qb = __builtin_amdgcn_alignbyte(D[i + 9], D[i + 8], al);       // ql[32 + l]
       const uint32_t hv = __builtin_amdgcn_alignbyte(D[18 + i], D[17 + i], al);     // qh[l]
-      const uint32_t va = opaque(((qa >> ns) & 0x0F0F0F0Fu) | (((hv >> s0) & 0x03030303u) << 4));
-      const uint32_t vb = opaque(((qb >> ns) & 0x0F0F0F0Fu) | (((hv >> s1) & 0x03030303u) << 4));
+      const uint32_t va = opaque(((qa >> ns) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(hv, hv, r0) & 0x30303030u));
+      const uint32_t vb = opaque(((qb >> ns) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(hv, hv, r1) & 0x30303030u));
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         acc[i >> 2] = __builtin_fmaf(x[4 * i + b], ubyte(va, b), acc[i >> 2]);
