@@ -569,3 +569,115 @@ def test_attention_vs_fp64(oracle, n_heads, n_kv, hs, rows, start):
             kc.reshape(rows, n_kv, hs)[:, h % n_kv]), np.ascontiguousarray(vc.reshape(rows, n_kv, hs)[:, h % n_kv]),
             1, 1, hs, rows - 1, start)[0] for h in range(n_heads)])
         assert not np.all(np.abs(bad - o64) <= 1e-5 * b64)
+
+
+# ------------------------------------------------------------------- MoE ---
+# Llama.kt:269-337 with MutableFloatTensor.kt:54-66.  The oracle's or_moe /
+# or_moe_exact are pinned three ways: (1) or_moe_exact against a numpy fp64
+# brute force over npref's independently decoded expert slabs (gate rows at
+# e*2*ff*dim, up rows after them, down at e*dim*ff), to 1e-12; (2) or_moe bit for
+# bit against its own composition from the pinned pieces (oracle.matmul at the
+# slab offsets, gelu, the product with up, saxpy in top-k order); (3) mutations
+# of the slab layout and of the gate weights, which the comparison must reject.
+
+def _gelu64(v: np.ndarray) -> np.ndarray:
+    v = v.astype(np.float64)
+    return 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v ** 3)))
+
+
+def _moe_fp64(t, gate_up, down, X, ids, w, dim, ff, gu_stride=None, swap_halves=False):
+    """numpy fp64 restatement of Llama.kt:300-337 from npref's decode.  Returns
+    (Y, scale) with scale = sum_j |w_j| sum_i |Wd[r, i] h_i| (the size of the
+    terms, for a relative tolerance)."""
+    GU = npref.dequant(t, gate_up).astype(np.float64)
+    DN = npref.dequant(t, down).astype(np.float64)
+    stride = 2 * ff * dim if gu_stride is None else gu_stride
+    T, k = ids.shape
+    Y = np.zeros((T, dim))
+    S = np.zeros((T, dim))
+    for tok in range(T):
+        x = X[tok].astype(np.float64)
+        for j in range(k):
+            e = int(ids[tok, j])
+            slab = GU[e * stride:e * stride + 2 * ff * dim].reshape(2 * ff, dim)
+            g, u = slab[:ff] @ x, slab[ff:] @ x
+            if swap_halves:
+                g, u = u, g
+            h = _gelu64(g) * u
+            Wd = DN[e * dim * ff:(e + 1) * dim * ff].reshape(dim, ff)
+            Y[tok] += float(w[tok, j]) * (Wd @ h)
+            S[tok] += abs(float(w[tok, j])) * (np.abs(Wd) @ np.abs(h))
+    return Y, S
+
+
+def _moe_case(E=6, dim=128, ff=64, T=3, k=3, seed=31):
+    gate_up = synth.q4_k(seed, "gu", E * 2 * ff * dim)
+    down = synth.q4_k(seed, "dn", E * dim * ff)
+    X = synth.activations(seed, "x", T * dim).reshape(T, dim)
+    logits = synth.activations(seed, "lg", T * E).reshape(T, E)
+    return gate_up, down, X, logits
+
+
+@pytest.mark.parametrize("E,dim,ff,T,k", [(4, 64, 64, 2, 2), (6, 128, 64, 3, 3), (8, 128, 64, 2, 3)])
+def test_moe_exact_matches_numpy_fp64(oracle, E, dim, ff, T, k):
+    gate_up, down, X, logits = _moe_case(E, dim, ff, T, k)
+    ids, w = oracle.route(logits, k, True)
+    y64, b64 = oracle.moe_exact(Q4_K, gate_up, Q4_K, down, X, ids, w, dim, ff)
+    ynp, scale = _moe_fp64(Q4_K, gate_up, down, X, ids, w, dim, ff)
+    assert np.all(np.abs(y64 - ynp) <= 1e-12 * scale + 1e-300)
+    # the fp32 restatement sits inside the propagated bound around the fp64 value
+    y32 = oracle.moe(Q4_K, gate_up, Q4_K, down, X, ids, w, dim, ff)
+    assert np.all(np.abs(y32 - ynp) <= 1e-5 * b64)
+
+
+def test_moe_routing_matches_numpy(oracle):
+    # softmax in double over all experts, top-k with ties to the lowest index,
+    # then (for the configuration's renormalised gates) w_j / sum of the k picks
+    _, _, _, logits = _moe_case(E=32, T=5)
+    k = 4
+    for renorm in (False, True):
+        ids, w = oracle.route(logits, k, renorm)
+        for t in range(logits.shape[0]):
+            l64 = logits[t].astype(np.float64)
+            p = np.exp(l64 - l64.max())
+            p = p / p.sum()
+            order = np.argsort(-p, kind="stable")[:k]
+            assert np.array_equal(ids[t], order)
+            want = p[order] / (p[order].sum() if renorm else 1.0)
+            assert np.allclose(w[t], want, rtol=1e-6, atol=0)
+
+
+def test_moe_is_the_composition(oracle):
+    E, dim, ff, T, k = 6, 128, 64, 3, 3
+    gate_up, down, X, logits = _moe_case(E, dim, ff, T, k)
+    ids, w = oracle.route(logits, k, True)
+    got = oracle.moe(Q4_K, gate_up, Q4_K, down, X, ids, w, dim, ff)
+    for tok in range(T):
+        out = np.zeros(dim, np.float32)
+        for j in range(k):
+            e = int(ids[tok, j])
+            gu = oracle.matmul(Q4_K, gate_up, X[tok], 2 * ff, dim, this_offset=e * 2 * ff * dim)
+            g, u = gu[:ff], gu[ff:]
+            h = np.array([oracle.gelu(float(v)) for v in g], np.float32) * u
+            dn = oracle.matmul(Q4_K, down, h, dim, ff, this_offset=e * dim * ff)
+            # saxpyInPlace: out[i] = a * that[i] + out[i], each step rounded to fp32
+            out = (np.float32(w[tok, j]) * dn + out).astype(np.float32)
+        assert same_bits(got[tok], out)
+
+
+@pytest.mark.parametrize("mutation", ["swap_gate_up", "gu_stride_ff_dim", "not_renormalised", "gates_misassigned"])
+def test_mutation_moe_layout_detected(oracle, mutation):
+    E, dim, ff, T, k = 6, 128, 64, 3, 3
+    gate_up, down, X, logits = _moe_case(E, dim, ff, T, k)
+    ids, w = oracle.route(logits, k, True)
+    y64, b64 = oracle.moe_exact(Q4_K, gate_up, Q4_K, down, X, ids, w, dim, ff)
+    if mutation == "swap_gate_up":
+        bad, _ = _moe_fp64(Q4_K, gate_up, down, X, ids, w, dim, ff, swap_halves=True)
+    elif mutation == "gu_stride_ff_dim":
+        bad, _ = _moe_fp64(Q4_K, gate_up, down, X, ids, w, dim, ff, gu_stride=ff * dim)
+    elif mutation == "not_renormalised":
+        _, w_raw = oracle.route(logits, k, False)
+        bad, _ = _moe_fp64(Q4_K, gate_up, down, X, ids, w_raw, dim, ff)
+    else:  # gate weight j applied to another slot's expert
+        bad, _ = _moe_fp64(Q4_K, gate_up, down, X, ids[:, ::-1].copy(), w, dim, ff)
+    assert not np.all(np.abs(bad - y64) <= 1e-5 * b64)
