@@ -587,11 +587,13 @@ G4_DEV void am_wave(float &v, int &i) {
 }
 
 
-// tanh(x) in double by fdlibm's algorithm (s_tanh.c), the one the JDK's
-// StrictMath.tanh (FdLibm.Tanh) runs and Math.tanh calls: |x| < 2^-55: x (1 + x);
-// |x| < 1: -t / (t + 2) with t = expm1(-2|x|); |x| < 22: 1 - 2 / (t + 2) with
-// t = expm1(2|x|); beyond: 1; then x's sign.  Near +-1, where gelu's 1 + tanh
-// keeps only the low bits, it is the correctly rounded double but in rare cases.
+// tanh(x) in double following the steps of fdlibm's s_tanh.c (the algorithm of
+// the JDK's StrictMath.tanh): |x| < 2^-55: x (1 + x); |x| < 1: -t / (t + 2) with
+// t = expm1(-2|x|); |x| < 22: 1 - 2 / (t + 2) with t = expm1(2|x|); beyond: 1;
+// then x's sign.  The expm1 is the device library's, not fdlibm's s_expm1.c, so
+// the last double bit can differ from StrictMath.tanh; the JVM's Math.tanh may
+// also run an intrinsic of its own.  Bit parity with the reference's tanh is
+// therefore not claimed: the result is within 2 ulps of tanh.
 G4_DEV double tanh_fdlibm(double x) {
   const double ax = fabs(x);
   if (x != x) return x + x;

@@ -235,6 +235,25 @@ def _dev_f32(t, name: str):
     return t
 
 
+def _dev_i32(t, name: str):
+    """A contiguous int32 device tensor (or a raw device address as int)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    import torch
+    if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.int32 and t.is_contiguous()):
+        raise IllegalArgumentException("%s must be a contiguous int32 device tensor" % name)
+    return t
+
+
+def _need(a, n: int, what: str) -> None:
+    """The reference indexes past the end of a short array with an exception
+    (IndexOutOfBoundsException); the C ABI would read or write past it."""
+    if a is not None and a.size < n:
+        raise IndexOutOfBoundsException("%s holds %d elements, %d needed" % (what, a.size, n))
+
+
 # ---------------------------------------------------------------- context ---
 
 
@@ -369,8 +388,10 @@ class GpuFloatTensor(FloatTensor):
     def matmul_argmax(self, that: np.ndarray, dim0: int, dim1: int, this_offset: int = 0,
                       logits: Optional[np.ndarray] = None) -> int:
         _f32(that, "that")
+        _need(that, dim1, "that")
         if logits is not None:
             _f32(logits, "logits")
+            _need(logits, dim0, "logits")
         idx = np.zeros(1, dtype=np.int32)
         check(lib().g4_matmul_argmax(self.ctx.handle, self.handle, int(this_offset), _ptr(that), _ptr(logits),
                                      _ptr(idx), int(dim0), int(dim1)))
@@ -379,7 +400,7 @@ class GpuFloatTensor(FloatTensor):
     def matmul_argmax_dev(self, that, logits, index, dim0: int, dim1: int, this_offset: int = 0) -> None:
         check(lib().g4_matmul_argmax_dev(self.ctx.handle, self.handle, int(this_offset),
                                          _ptr(_dev_f32(that, "that")), _ptr(_dev_f32(logits, "logits")),
-                                         _ptr(index), int(dim0), int(dim1)))
+                                         _ptr(_dev_i32(index, "index")), int(dim0), int(dim1)))
 
 
 class FloatTensorFactory:
@@ -415,6 +436,7 @@ def ffn(ctx: Context, gate: GpuFloatTensor, up: GpuFloatTensor, down: GpuFloatTe
         dim: int, hidden: int) -> np.ndarray:
     """y = down(gelu(gate x) * up x) (Llama.kt:357-361)."""
     _f32(x, "x")
+    _need(x, dim, "x")
     y = np.empty(dim, dtype=np.float32)
     check(lib().g4_ffn(ctx.handle, gate.handle, up.handle, down.handle, _ptr(x), _ptr(y), int(dim), int(hidden)))
     return y
@@ -429,6 +451,7 @@ def ffn_gate_up(ctx: Context, gate: GpuFloatTensor, up: GpuFloatTensor, x: np.nd
                 hidden: int) -> np.ndarray:
     """h = gelu(gate x) * (up x) (Llama.kt:357-360)."""
     _f32(x, "x")
+    _need(x, dim, "x")
     h = np.empty(hidden, dtype=np.float32)
     check(lib().g4_ffn_gate_up(ctx.handle, gate.handle, up.handle, _ptr(x), _ptr(h), int(dim), int(hidden)))
     return h
@@ -448,6 +471,7 @@ def moe_route(ctx: Context, logits: np.ndarray, k: int, renormalize: bool,
     w = np.zeros((T, k), dtype=np.float32)
     if expert_scale is not None:
         _f32(expert_scale, "expert_scale")
+        _need(expert_scale, E, "expert_scale")
     check(lib().g4_moe_route(ctx.handle, _ptr(logits), int(T), int(E), int(k), int(bool(renormalize)),
                              _ptr(expert_scale), _ptr(ids), _ptr(w)))
     return ids, w
@@ -457,7 +481,7 @@ def moe_route_dev(ctx: Context, logits, T: int, n_experts: int, k: int, renormal
                   expert_scale=None) -> None:
     check(lib().g4_moe_route_dev(ctx.handle, _ptr(_dev_f32(logits, "logits")), int(T), int(n_experts), int(k),
                                  int(bool(renormalize)), _ptr(_dev_f32(expert_scale, "expert_scale")),
-                                 _ptr(ids), _ptr(_dev_f32(weights, "weights"))))
+                                 _ptr(_dev_i32(ids, "ids")), _ptr(_dev_f32(weights, "weights"))))
 
 
 def moe(ctx: Context, gate_up: GpuFloatTensor, down: GpuFloatTensor, X: np.ndarray, ids: np.ndarray,
@@ -467,7 +491,12 @@ def moe(ctx: Context, gate_up: GpuFloatTensor, down: GpuFloatTensor, X: np.ndarr
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     weights = _f32(np.ascontiguousarray(weights, dtype=np.float32), "weights")
     T = X.size // dim
+    if X.size != T * dim:
+        raise IllegalArgumentException("X holds %d floats, not a whole number of dim %d rows" % (X.size, dim))
     k = ids.size // T if T else 0
+    if ids.size != T * k or weights.size != ids.size:
+        raise IndexOutOfBoundsException("ids (%d) and weights (%d) must hold T*k entries for T = %d"
+                                        % (ids.size, weights.size, T))
     Y = np.empty((T, dim), dtype=np.float32)
     check(lib().g4_moe(ctx.handle, gate_up.handle, down.handle, _ptr(X), int(T), int(dim), int(ff), _ptr(ids),
                        _ptr(weights), int(k), _ptr(Y)))
@@ -476,7 +505,7 @@ def moe(ctx: Context, gate_up: GpuFloatTensor, down: GpuFloatTensor, X: np.ndarr
 
 def moe_dev(ctx: Context, gate_up, down, X, T: int, dim: int, ff: int, ids, weights, k: int, Y) -> None:
     check(lib().g4_moe_dev(ctx.handle, gate_up.handle, down.handle, _ptr(_dev_f32(X, "X")), int(T), int(dim),
-                           int(ff), _ptr(ids), _ptr(_dev_f32(weights, "weights")), int(k),
+                           int(ff), _ptr(_dev_i32(ids, "ids")), _ptr(_dev_f32(weights, "weights")), int(k),
                            _ptr(_dev_f32(Y, "Y"))))
 
 
@@ -491,6 +520,7 @@ def moe_routed(ctx: Context, gate_up: GpuFloatTensor, down: GpuFloatTensor, X: n
         raise ValueError("X holds %d floats, %d tokens x dim %d need %d" % (X.size, T, dim, T * dim))
     if expert_scale is not None:
         expert_scale = _f32(np.ascontiguousarray(expert_scale, dtype=np.float32), "expert_scale")
+        _need(expert_scale, E, "expert_scale")
     ids = np.zeros((T, k), dtype=np.int32)
     w = np.zeros((T, k), dtype=np.float32)
     Y = np.empty((T, dim), dtype=np.float32)
@@ -504,7 +534,8 @@ def moe_routed_dev(ctx: Context, gate_up, down, X, T: int, dim: int, ff: int, lo
                    renormalize: bool, ids, weights, Y, expert_scale=None) -> None:
     check(lib().g4_moe_routed_dev(ctx.handle, gate_up.handle, down.handle, _ptr(_dev_f32(X, "X")), int(T),
                                   int(dim), int(ff), _ptr(_dev_f32(logits, "logits")), int(n_experts), int(k),
-                                  int(bool(renormalize)), _ptr(_dev_f32(expert_scale, "expert_scale")), _ptr(ids),
+                                  int(bool(renormalize)), _ptr(_dev_f32(expert_scale, "expert_scale")),
+                                  _ptr(_dev_i32(ids, "ids")),
                                   _ptr(_dev_f32(weights, "weights")), _ptr(_dev_f32(Y, "Y"))))
 
 
@@ -555,6 +586,7 @@ def ffn_block(ctx: Context, gate: GpuFloatTensor, up: GpuFloatTensor, down: GpuF
               eps: float) -> np.ndarray:
     """Dense FFN block of Llama.kt:355-363; returns the updated residual stream x."""
     x = _f32(np.array(x, dtype=np.float32, copy=True), "x")
+    _need(x, dim, "x")
     check(lib().g4_ffn_block(ctx.handle, gate.handle, up.handle, down.handle, norm_pre.handle, norm_post.handle,
                              _ptr(x), int(dim), int(hidden), float(eps)))
     return x
@@ -569,6 +601,7 @@ def lm_head(ctx: Context, w_cls: GpuFloatTensor, norm_final: GpuFloatTensor, x: 
             eps: float, softcap: float, want_logits: bool = True):
     """Llama.kt:401-407 then Sampler.ARGMAX: (logits or None, index)."""
     _f32(x, "x")
+    _need(x, dim, "x")
     logits = np.empty(vocab, dtype=np.float32) if want_logits else None
     idx = np.zeros(1, dtype=np.int32)
     check(lib().g4_lm_head(ctx.handle, w_cls.handle, norm_final.handle, _ptr(x), _ptr(logits), _ptr(idx),
@@ -579,7 +612,8 @@ def lm_head(ctx: Context, w_cls: GpuFloatTensor, norm_final: GpuFloatTensor, x: 
 def lm_head_dev(ctx: Context, w_cls, norm_final, x, logits, index, vocab: int, dim: int, eps: float,
                 softcap: float, xnorm=None) -> None:
     check(lib().g4_lm_head_dev(ctx.handle, w_cls.handle, norm_final.handle, _ptr(_dev_f32(x, "x")),
-                               _ptr(_dev_f32(xnorm, "xnorm")), _ptr(_dev_f32(logits, "logits")), _ptr(index),
+                               _ptr(_dev_f32(xnorm, "xnorm")), _ptr(_dev_f32(logits, "logits")),
+                               _ptr(_dev_i32(index, "index")),
                                int(vocab), int(dim), float(eps), float(softcap)))
 
 

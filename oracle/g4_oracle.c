@@ -586,10 +586,13 @@ void or_route(const float *logits, int32_t n_experts, int32_t k, int renormalize
   free(p);
 }
 
-/* kotlin.math.tanh = java.lang.Math.tanh, which calls StrictMath.tanh: fdlibm's
-   algorithm (s_tanh.c; the JDK's FdLibm.Tanh): |x| < 2^-55: x * (1 + x);
-   |x| < 1: -t / (t + 2), t = expm1(-2|x|); |x| < 22: 1 - 2 / (t + 2),
-   t = expm1(2|x|); beyond: 1; then x's sign.  expm1 is the C library's. */
+/* kotlin.math.tanh = java.lang.Math.tanh (Llama.kt:23-25 gelu, :403-406 soft-cap).
+   Restated with the steps of fdlibm's s_tanh.c (the algorithm of the JDK's
+   StrictMath.tanh): |x| < 2^-55: x * (1 + x); |x| < 1: -t / (t + 2),
+   t = expm1(-2|x|); |x| < 22: 1 - 2 / (t + 2), t = expm1(2|x|); beyond: 1; then
+   x's sign.  expm1 is the C library's, not fdlibm's s_expm1.c, and the JVM may
+   run an intrinsic for Math.tanh, so bit parity with the reference's tanh is
+   unpinned; the function is pinned to within 2 ulps of tanh. */
 double or_tanh(double x) {
   const double ax = fabs(x);
   double z = 1.0;

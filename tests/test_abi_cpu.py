@@ -138,3 +138,62 @@ def test_python_errors_map_to_reference_exceptions(g4):
     assert issubclass(g4.IllegalArgumentException, ValueError)
     with pytest.raises(g4.IllegalArgumentException):
         g4._f32(np.zeros(3, np.float64), "x")
+
+
+def _fake_tensor(g4):
+    """A GpuFloatTensor shell with no device behind it: the wrappers' argument
+    checks run before any library call, so a short array must raise here."""
+    t = object.__new__(g4.GpuFloatTensor)
+    t.ctx, t.handle, t.size = type("C", (), {"handle": None})(), None, 0
+    return t
+
+
+def test_short_host_arrays_raise_index_out_of_bounds(g4):
+    ctx = type("C", (), {"handle": None})()
+    w = _fake_tensor(g4)
+    short = np.zeros(7, np.float32)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        w.matmul(short, np.zeros(8, np.float32), 8, 8)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        w.matmul(np.zeros(8, np.float32), short, 8, 8)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        w.matmul_argmax(short, 8, 8)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        w.matmul_argmax(np.zeros(8, np.float32), 8, 8, logits=short)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        g4.ffn(ctx, w, w, w, short, 8, 16)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        g4.ffn_gate_up(ctx, w, w, short, 8, 16)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        g4.ffn_block(ctx, w, w, w, w, w, short, 8, 16, 1e-6)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        g4.lm_head(ctx, w, w, short, 32, 8, 1e-6, 0.0)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        g4.moe_route(ctx, np.zeros((2, 8), np.float32), 2, True, expert_scale=short)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        g4.moe_routed(ctx, w, w, np.zeros((2, 8), np.float32), np.zeros((2, 8), np.float32), 2, True, 8, 4,
+                      expert_scale=short)
+    # ids and weights of different lengths, or not T*k entries
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        g4.moe(ctx, w, w, np.zeros((2, 8), np.float32), np.zeros((2, 3), np.int32), np.zeros(5, np.float32), 8, 4)
+    with pytest.raises(g4.IndexOutOfBoundsException):
+        g4.moe(ctx, w, w, np.zeros((2, 8), np.float32), np.zeros(5, np.int32), np.zeros(5, np.float32), 8, 4)
+    with pytest.raises(g4.IllegalArgumentException):
+        g4.moe(ctx, w, w, np.zeros(17, np.float32), np.zeros((2, 3), np.int32), np.zeros((2, 3), np.float32), 8, 4)
+
+
+def test_device_index_arguments_must_be_int32_device_tensors(g4):
+    import torch
+    ctx = type("C", (), {"handle": None})()
+    w = _fake_tensor(g4)
+    for bad in (np.zeros(1, np.int32), torch.zeros(1, dtype=torch.int64), torch.zeros(1, dtype=torch.int32)):
+        # host memory (numpy, or a CPU tensor) would hand the kernel a host address
+        with pytest.raises(g4.IllegalArgumentException):
+            g4._dev_i32(bad, "index")
+        with pytest.raises(g4.IllegalArgumentException):
+            w.matmul_argmax_dev(None, None, bad, 8, 8)
+        with pytest.raises(g4.IllegalArgumentException):
+            g4.moe_route_dev(ctx, None, 1, 8, 2, True, bad, None)
+        with pytest.raises(g4.IllegalArgumentException):
+            g4.lm_head_dev(ctx, w, w, None, None, bad, 8, 8, 1e-6, 0.0)
+    assert g4._dev_i32(1234, "raw address") == 1234

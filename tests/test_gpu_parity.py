@@ -286,7 +286,7 @@ def _ffn_reference(oracle, c):
 
 
 def test_gelu_through_identity_gate_up(g4, ctx, oracle):
-    """gelu itself (Llama.kt:23-25, tanh of StrictMath.tanh in double): with BF16
+    """gelu itself (Llama.kt:23-25, a double tanh by fdlibm's steps): with BF16
     identity gate and up matrices, h_i = gelu(x_i) * x_i exactly, so h is compared
     bit for bit with the oracle's gelu over x spanning its regimes (cancellation of
     1 + tanh near x = -6, saturation, tiny and huge x).  The device's expm1 and the
