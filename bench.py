@@ -95,6 +95,14 @@ class Workload:
         """Launch only the dominant kernel of step i (for its roofline timing)."""
         self.step(i)
 
+    def set_steps(self, steps: int) -> None:
+        """The timed region runs steps 0 .. steps-1 (workloads whose bytes differ per step adjust)."""
+
+    def parts(self) -> list:
+        """(kernel name, algorithmic bytes per launch, launch fn(i)) of each launch of
+        a step that is timed on its own; by default the dominant kernel only."""
+        return [(self.dominant_name, self.dominant_bytes, self.dominant)]
+
     # The same step through the host-pointer entry point (activations copied in,
     # results copied out, synchronous), timed apart from `value`; None: no such call.
     host_step = None
@@ -109,6 +117,7 @@ class Workload:
 class FfnQ4_0(Workload):
     name = "q4_0_ffn_decode_token"
     dominant_name = "k_rows<FmtQ4_0, 32, EPI_GELU_PAIR> (gate+up fused)"
+    down_name = "k_rows<FmtQ4_0, 64, EPI_STORE> (down)"
 
     def __init__(self, g4, ctx, torch):
         import synth
@@ -144,6 +153,15 @@ class FfnQ4_0(Workload):
     def dominant(self, i):
         wg, wu, _ = self.w[i % self.copies]
         self.g4.ffn_gate_up_dev(self.ctx, wg, wu, self.x, self.h, self.dim, self.hidden)
+
+    def down(self, i):
+        self.w[i % self.copies][2].matmul_dev(self.h, self.y, self.dim, self.hidden)
+
+    def parts(self):
+        # the down launch: W_down, h read once, y written once
+        down_bytes = self.c["down"].nbytes + 4 * self.hidden + 4 * self.dim
+        return [(self.dominant_name, self.dominant_bytes, self.dominant),
+                (self.down_name, down_bytes, self.down)]
 
     def cpu_setup(self, oracle):
         self.oracle = oracle
@@ -319,6 +337,13 @@ class MoeQ4_K(Workload):
         self.tokens_per_step = tokens
         self.g4, self.ctx = g4, ctx
 
+    def set_steps(self, steps):
+        # the routings the timed steps use (step i takes routing i mod copies)
+        used = [self.distinct[i % self.copies] for i in range(steps)]
+        self.mean_used = float(np.mean(used))
+        self.step_bytes = int(self.mean_used * self.per_expert + 4 * self.T * (self.D + self.E + self.D))
+        self.dominant_bytes = self.step_bytes
+
     def step(self, i):
         # routing (inside the gate_up launch), experts and the weighted sum
         r = i % self.copies
@@ -339,7 +364,8 @@ class MoeQ4_K(Workload):
 
     def config(self):
         return {"workload": self.name, "format": "Q4_K", "experts": self.E, "top_k": self.K, "tokens": self.T,
-                "routings": self.copies, "mean_distinct_experts": float(np.mean(self.distinct)),
+                "routings": self.copies,
+                "mean_distinct_experts": getattr(self, "mean_used", float(np.mean(self.distinct))),
                 "algorithmic_bytes_per_step": self.step_bytes}
 
 
@@ -603,20 +629,50 @@ def cpu_baseline(wl: Workload, seconds: float) -> dict:
     return {"value": round(value, 3), "unit": wl.unit, "cores": threads, "kind": "port", "sample": sample}
 
 
-def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool) -> dict:
+def _time_parts(wl, ctx, stream, torch, copies: int, use_graph: bool, capture) -> list:
+    """Average launch time of each separately timed launch of a step: HIP events on
+    the launch stream around back-to-back graph replays of that launch alone,
+    cycling the weight copies (at least 64 launches)."""
+    out = []
+    reps = max(1, math.ceil(64 / copies))
+    for name, nbytes, fn in wl.parts():
+        g = None
+        if use_graph:
+            try:
+                g = capture(lambda: [fn(i) for i in range(copies)])
+            except Exception:
+                g = None
+                torch.cuda.synchronize()
+        ctx.set_stream(stream.cuda_stream)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for _ in range(reps):
+            if g is not None:
+                g.replay()
+            else:
+                for i in range(copies):
+                    fn(i)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3 / (reps * copies)
+        out.append({"kernel": name, "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3),
+                    "launches_timed": reps * copies})
+    return out
+
+
+def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool, ctx=None) -> dict:
     import torch
     import g4hip as g4
     if g4.device_count() == 0:
         raise SystemExit("bench.py needs a HIP device")
     torch.cuda.init()
-    ctx = g4.Context(0)
+    own_ctx = ctx is None
+    if own_ctx:
+        ctx = g4.Context(0)
     wl = make_workload(spec, g4, ctx, torch)
     stream = torch.cuda.Stream()
-    # one graph replays whole passes over the weight copies, at least GRAPH_MIN_STEPS steps
+    # graphs of part timings replay whole passes over the weight copies
     copies = wl.copies * max(1, math.ceil(GRAPH_MIN_STEPS / wl.copies))
-    rounds = max(1, math.ceil(steps / copies))
-    steps = rounds * copies
-    dom_rounds = max(1, math.ceil(64 / copies))
 
     def capture(fn):
         g = torch.cuda.CUDAGraph()
@@ -632,41 +688,33 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool)
         for i in range(warmup):
             wl.step(i)
         torch.cuda.synchronize()
-        step_graph = dom_graph = None
+        # the timed region is exactly `steps` steps, step i on weight copy / routing
+        # i mod copies, captured as one graph (one replay: the graph's own launch
+        # cost is spread over the steps as in a decode loop); the capture is
+        # replayed once untimed first
+        step_graph = None
+        wl.set_steps(steps)
         if use_graph:
             try:
-                step_graph = capture(lambda: [wl.step(i) for i in range(copies)])
-                dom_graph = capture(lambda: [wl.dominant(i) for i in range(copies)])
+                step_graph = capture(lambda: [wl.step(i) for i in range(steps)])
             except Exception as e:
                 print("graph capture unavailable (%s); timing eager launches" % str(e).splitlines()[0],
                       file=sys.stderr)
-                step_graph = dom_graph = None
+                step_graph = None
                 torch.cuda.synchronize()
         ctx.set_stream(stream.cuda_stream)
-        # timed region: `steps` steps, device-synchronised on both sides
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(rounds):
-            if step_graph is not None:
-                step_graph.replay()
-            else:
-                for i in range(copies):
-                    wl.step(i)
+        if step_graph is not None:
+            step_graph.replay()
+        else:
+            for i in range(steps):
+                wl.step(i)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
-        # dominant kernel: HIP events on the launch stream around back-to-back launches
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        ev0.record(stream)
-        for _ in range(dom_rounds):
-            if dom_graph is not None:
-                dom_graph.replay()
-            else:
-                for i in range(copies):
-                    wl.dominant(i)
-        ev1.record(stream)
-        torch.cuda.synchronize()
-        launches = dom_rounds * copies
-        kern_ms = ev0.elapsed_time(ev1) / launches
+        graphed = step_graph is not None
+        del step_graph
+        parts = _time_parts(wl, ctx, stream, torch, copies, use_graph, capture)
         ctx.set_stream(None)
     # the host-pointer entry point of the same step (copies in and out, synchronous;
     # not part of `value`): after a few untimed calls, the mean over whole passes
@@ -686,9 +734,15 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool)
     else:
         value = wl.step_bytes / (ms_per_step / 1e3) / 1e9
         gbs_step = value
-    achieved = wl.dominant_bytes / (kern_ms / 1e3) / 1e9
+    for p in parts:
+        gbs = p["bytes_per_launch"] / (p["avg_launch_us"] / 1e6) / 1e9
+        p["achieved_gbs"] = round(gbs, 2)
+        p["frac"] = round(gbs / HBM_PEAK_GBS, 4)
+    dom = parts[0]
+    kern_s = dom["avg_launch_us"] / 1e6
+    achieved = wl.dominant_bytes / kern_s / 1e9
     if wl.bound == "mfma":
-        tflops = wl.dominant_flops / (kern_ms / 1e3) / 1e12
+        tflops = wl.dominant_flops / kern_s / 1e12
         roofline = {"bound": "mfma", "achieved": round(tflops, 3), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5), "traffic": TRAFFIC_BYTES.get(wl.name),
                     "hbm_gbs": round(achieved, 2), "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -697,7 +751,9 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool)
         roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES.get(wl.name)}
     roofline.update({"kernel": wl.dominant_name, "bytes_per_launch": wl.dominant_bytes,
-                     "avg_launch_us": round(kern_ms * 1e3, 3), "launches_timed": launches})
+                     "avg_launch_us": dom["avg_launch_us"], "launches_timed": dom["launches_timed"]})
+    if len(parts) > 1:
+        roofline["step_kernels"] = parts
     line = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -711,7 +767,7 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool)
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: seeded GGUF blocks and activations (gemma4.kt_amd/synth.py)",
-        "config": dict(wl.config(), graph=step_graph is not None, step_gbs=round(gbs_step, 2),
+        "config": dict(wl.config(), graph=graphed, step_gbs=round(gbs_step, 2),
                        hbm_fraction=round(gbs_step / HBM_PEAK_GBS, 4)),
         # host-pointer calls (activations over PCIe each call), reported apart from value
         "host_pointer_call": None if host_us is None else {
@@ -723,8 +779,32 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool)
     }
     if cpu_seconds > 0 and not isinstance(wl, CopyCalibration):
         line["cpu_baseline"] = cpu_baseline(wl, cpu_seconds)
-    ctx.close()
+    del wl
+    torch.cuda.synchronize()
+    if own_ctx:
+        ctx.close()
     return line
+
+
+# Every other configuration the metric is quoted on, measured in the same run
+# and reported in the default line's per_config object.
+PER_CONFIG = ["q8_0_matvec", "q8_0_lm_head", "q4_k_batched:1", "q4_k_batched:8", "q4_k_batched:32",
+              "q4_k_batched:64", "moe:1", "moe:16"]
+
+
+def compact(line: dict) -> dict:
+    """The per_config entry of one workload's line."""
+    r = line["roofline"]
+    c = {"workload": line["config"]["workload"], "value": line["value"], "unit": line["unit"],
+         "ms_per_step": line["ms_per_step"], "steps": line["steps"], "step_gbs": line["config"]["step_gbs"],
+         "hbm_fraction": line["config"]["hbm_fraction"],
+         "roofline": {k: r[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic", "kernel",
+                                        "avg_launch_us") if k in r}}
+    if "hbm_gbs" in r:
+        c["roofline"]["hbm_gbs"], c["roofline"]["hbm_frac"] = r["hbm_gbs"], r["hbm_frac"]
+    if "cpu_baseline" in line:
+        c["cpu_baseline"] = line["cpu_baseline"]
+    return c
 
 
 def main():
@@ -736,6 +816,10 @@ def main():
     ap.add_argument("--all", action="store_true", help="one JSON line per workload")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (0 = skip)")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
+    ap.add_argument("--no-per-config", action="store_true",
+                    help="skip the other configurations in the default line's per_config object")
+    ap.add_argument("--per-config-cpu-seconds", type=float, default=2.0,
+                    help="CPU baseline sample length of each per_config entry")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each box has one MI355X); "
@@ -746,8 +830,18 @@ def main():
         specs = ["q4_0_ffn", "q8_0_matvec", "q8_0_lm_head", "q4_k_batched:1", "q4_k_batched:8",
                  "q4_k_batched:32", "q4_k_batched:64", "moe:1", "moe:16", "q5_k_matvec", "q6_k_matvec",
                  "q4_0_ffn_block", "q8_0_lm_head_cap", "attention:8192"]
+    if args.steps < 1:
+        raise SystemExit("--steps must be at least 1")
+    default = not args.all and args.workload == "q4_0_ffn"
     for s in specs:
         line = run(s, args.steps, args.warmup, args.cpu_seconds, not args.eager)
+        if default and not args.no_per_config:
+            per = {}
+            for spec in PER_CONFIG:
+                print("per_config: %s" % spec, file=sys.stderr, flush=True)
+                sub = run(spec, args.steps, args.warmup, args.per_config_cpu_seconds, not args.eager)
+                per[sub["config"]["workload"]] = compact(sub)
+            line["per_config"] = per
         print(json.dumps(line), flush=True)
 
 

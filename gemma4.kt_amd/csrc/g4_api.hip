@@ -29,6 +29,14 @@ struct g4_ctx {
   g4::DevInfo dev;
   char *scratch;  // grow-only device buffer for staging and intermediates
   size_t scratch_bytes;
+  // Stream capture: a captured graph keeps the scratch addresses it was recorded
+  // with, so once any call on this context has been captured, a buffer that is
+  // outgrown is retired (kept until g4_close) instead of freed, and no call may
+  // grow the scratch while its stream is capturing (hipMalloc is not capturable).
+  bool capturing;  // the current call's stream is capturing
+  bool captured;   // some call on this context was captured
+  char *retired[32];
+  int n_retired;
   float *am_val;  // per-block argmax partials and a result slot
   int32_t *am_idx;
   int32_t *am_out;
@@ -98,9 +106,15 @@ size_t up(size_t n) { return (n + ALIGN - 1) & ~(ALIGN - 1); }
 
 int use_device(g4_ctx *ctx) {
   G4_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  G4_HIP(hipStreamIsCapturing(ctx->stream, &st), "hipStreamIsCapturing");
+  ctx->capturing = st != hipStreamCaptureStatusNone;
+  if (ctx->capturing) ctx->captured = true;
   // a host-pointer call that failed part way leaves staged results behind: they
   // are dropped (the call reported its error) once its queued work is done
   if (ctx->pin_used || ctx->n_outs) {
+    if (ctx->capturing)
+      return fail(G4_ERR_INVALID_ARGUMENT, "a failed host-pointer call left work queued: synchronise before capturing");
     G4_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     ctx->pin_used = 0;
     ctx->n_outs = 0;
@@ -108,18 +122,54 @@ int use_device(g4_ctx *ctx) {
   return G4_OK;
 }
 
-// Make sure the context's scratch holds `bytes`; waits for queued work before a regrow.
+// Host-pointer entry points copy through pinned memory and synchronise, which a
+// stream capture cannot record.
+int use_host(g4_ctx *ctx) {
+  const int rc = use_device(ctx);
+  if (rc != G4_OK) return rc;
+  if (ctx->capturing)
+    return fail(G4_ERR_INVALID_ARGUMENT,
+                "host-pointer calls synchronise and cannot run under stream capture (use the *_dev entry points)");
+  return G4_OK;
+}
+
+// Make sure the context's scratch holds `bytes`.  Before any capture: waits for
+// queued work, frees the old buffer and allocates the new one.  After a capture:
+// the old buffer stays allocated (a graph may still replay into it) until
+// g4_close.  During a capture: an error, since the allocation cannot be captured.
 int ensure_scratch(g4_ctx *ctx, size_t bytes) {
   if (bytes <= ctx->scratch_bytes) return G4_OK;
+  if (ctx->capturing)
+    return fail(G4_ERR_INVALID_ARGUMENT,
+                "the call needs %zu bytes of context scratch, %zu are reserved, and its stream is being captured: "
+                "reserve them before the capture (g4_ctx_reserve)", bytes, ctx->scratch_bytes);
+  size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+  if (ctx->captured) {
+    if (ctx->n_retired == (int)(sizeof(ctx->retired) / sizeof(ctx->retired[0])))
+      return fail(G4_ERR_OUT_OF_MEMORY, "context scratch regrown too often after a capture");
+    if (want < 2 * ctx->scratch_bytes) want = 2 * ctx->scratch_bytes;  // few retirements
+    void *p = nullptr;
+    G4_HIP(hipMalloc(&p, want), "hipMalloc(scratch)");
+    if (ctx->scratch) ctx->retired[ctx->n_retired++] = ctx->scratch;
+    ctx->scratch = (char *)p;
+    ctx->scratch_bytes = want;
+    return G4_OK;
+  }
   G4_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
   if (ctx->scratch) G4_HIP(hipFree(ctx->scratch), "hipFree");
   ctx->scratch = nullptr;
   ctx->scratch_bytes = 0;
-  size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
   void *p = nullptr;
   G4_HIP(hipMalloc(&p, want), "hipMalloc(scratch)");
   ctx->scratch = (char *)p;
   ctx->scratch_bytes = want;
+  return G4_OK;
+}
+
+// Zero `bytes` of device memory by a kernel (a memset node in a captured graph
+// is avoided: the degenerate shapes below may run under capture).
+int zero_dev(g4_ctx *ctx, void *p, size_t bytes) {
+  G4_HIP(g4::launch_zero(p, bytes, ctx->stream), "zero fill");
   return G4_OK;
 }
 
@@ -288,7 +338,7 @@ int matmul_dev(g4_ctx *ctx, const g4_weight *w, int64_t off, const float *d_x, f
                int32_t dim1) {
   if (dim0 == 0) return G4_OK;
   if (dim1 == 0) {
-    G4_HIP(hipMemsetAsync(d_y, 0, sizeof(float) * (size_t)dim0, ctx->stream), "hipMemsetAsync");
+    G4_TRY(zero_dev(ctx, d_y, sizeof(float) * (size_t)dim0));
     return G4_OK;
   }
   g4::RowsArgs a = plain_rows(w, off, d_x, d_y, dim0, dim1);
@@ -324,7 +374,7 @@ int batch_dev(g4_ctx *ctx, const g4_weight *w, int64_t off, const float *d_X, in
               int32_t dim1, float *d_part) {
   if (dim0 == 0 || M == 0) return G4_OK;
   if (dim1 == 0) {
-    G4_HIP(hipMemsetAsync(d_Y, 0, sizeof(float) * (size_t)dim0 * M, ctx->stream), "hipMemsetAsync");
+    G4_TRY(zero_dev(ctx, d_Y, sizeof(float) * (size_t)dim0 * M));
     return G4_OK;
   }
   // several tokens: the matrix-core kernel unpacks each weight once for all of them
@@ -417,7 +467,7 @@ int moe_dev(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t n_e
             float *d_ys, float *d_gu, const MoeRoute *route = nullptr) {
   const int32_t S = T * k;  // (token, slot) pairs
   if (S == 0) {
-    if (T > 0) G4_HIP(hipMemsetAsync(d_Y, 0, sizeof(float) * (size_t)T * dim, ctx->stream), "hipMemsetAsync");
+    if (T > 0) G4_TRY(zero_dev(ctx, d_Y, sizeof(float) * (size_t)T * dim));
     return G4_OK;
   }
   g4::RowsArgs a;
@@ -678,6 +728,7 @@ int g4_close(g4_ctx *ctx) {
   (void)hipStreamSynchronize(ctx->stream);
   (void)hipStreamSynchronize(ctx->own_stream);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
+  for (int i = 0; i < ctx->n_retired; ++i) (void)hipFree(ctx->retired[i]);
   if (ctx->am_val) (void)hipFree(ctx->am_val);
   if (ctx->pin) (void)hipHostFree(ctx->pin);
   (void)hipStreamDestroy(ctx->own_stream);
@@ -693,8 +744,22 @@ int g4_ctx_set_stream(g4_ctx *ctx, void *stream) {
 
 int g4_ctx_sync(g4_ctx *ctx) {
   G4_TRY(check_ctx(ctx));
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   return finish(ctx);
+}
+
+int g4_ctx_reserve(g4_ctx *ctx, int64_t bytes) {
+  G4_TRY(check_ctx(ctx));
+  if (bytes < 0) return fail(G4_ERR_INVALID_ARGUMENT, "negative reservation %lld", (long long)bytes);
+  G4_TRY(use_device(ctx));
+  return ensure_scratch(ctx, (size_t)bytes);
+}
+
+int g4_ctx_scratch_bytes(const g4_ctx *ctx, int64_t *bytes) {
+  G4_TRY(check_ctx(ctx));
+  if (!bytes) return fail(G4_ERR_INVALID_ARGUMENT, "bytes is null");
+  *bytes = (int64_t)ctx->scratch_bytes;
+  return G4_OK;
 }
 
 int g4_ctx_device(const g4_ctx *ctx, int *ordinal) {
@@ -718,7 +783,7 @@ int g4_upload(g4_ctx *ctx, int ggml_type, const void *raw, int64_t nbytes, int64
     return fail(G4_ERR_INVALID_ARGUMENT, "nbytes %lld != byteSizeFor(%lld) = %lld", (long long)nbytes,
                 (long long)n_elems, (long long)want);
   if (!raw && nbytes > 0) return fail(G4_ERR_INVALID_ARGUMENT, "raw is null");
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   void *d = nullptr;
   const size_t alloc = (size_t)nbytes + ALIGN;  // zeroed tail: no load ever reads past a block, kept as margin
   G4_HIP(hipMalloc(&d, alloc), "hipMalloc(weight)");
@@ -774,7 +839,7 @@ int g4_matmul(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const float 
   G4_TRY(check_rows(w, this_offset, dim0, dim1));
   if ((!that && dim1 > 0) || (!out && dim0 > 0)) return fail(G4_ERR_INVALID_ARGUMENT, "that/out is null");
   if (dim0 == 0) return ok();
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t ox = c.add(sizeof(float) * (size_t)dim1), oy = c.add(sizeof(float) * (size_t)dim0);
   G4_TRY(ensure_scratch(ctx, c.off));
@@ -807,7 +872,7 @@ int g4_matmul_batch(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const 
   if (M > 65535) return fail(G4_ERR_INVALID_ARGUMENT, "M %d exceeds 65535", M);
   if ((!X && M > 0 && dim1 > 0) || (!Y && M > 0 && dim0 > 0)) return fail(G4_ERR_INVALID_ARGUMENT, "X/Y is null");
   if (M == 0 || dim0 == 0) return ok();
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t ox = c.add(sizeof(float) * (size_t)dim1 * M), oy = c.add(sizeof(float) * (size_t)dim0 * M);
   size_t op = c.add(sizeof(float) * (size_t)batch_part_floats(ctx, w, this_offset, M, dim0, dim1));
@@ -843,7 +908,7 @@ int g4_matmul_argmax(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const
   G4_TRY(check_rows(w, this_offset, dim0, dim1));
   if (dim0 <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "argmax needs dim0 > 0 (FloatTensor.kt:54)");
   if ((!that && dim1 > 0) || !index) return fail(G4_ERR_INVALID_ARGUMENT, "that/index is null");
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t ox = c.add(sizeof(float) * (size_t)dim1), oy = c.add(sizeof(float) * (size_t)dim0),
          oi = c.add(sizeof(int32_t));
@@ -852,7 +917,7 @@ int g4_matmul_argmax(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, const
   int32_t *di = (int32_t *)(ctx->scratch + oi);
   G4_TRY(copy_in(ctx, dx, that, sizeof(float) * (size_t)dim1));
   if (dim1 == 0) {
-    G4_HIP(hipMemsetAsync(dy, 0, sizeof(float) * (size_t)dim0, ctx->stream), "hipMemsetAsync");
+    G4_TRY(zero_dev(ctx, dy, sizeof(float) * (size_t)dim0));
     G4_TRY(launch_status(g4::launch_argmax(dy, dim0, ctx->am_val, ctx->am_idx, di, ctx->dev,
                                            ctx->stream), "argmax"));
   } else {
@@ -879,7 +944,7 @@ int g4_matmul_argmax_dev(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, c
     dy = (float *)(ctx->scratch + oy);
   }
   if (dim1 == 0) {
-    G4_HIP(hipMemsetAsync(dy, 0, sizeof(float) * (size_t)dim0, ctx->stream), "hipMemsetAsync");
+    G4_TRY(zero_dev(ctx, dy, sizeof(float) * (size_t)dim0));
     return launch_status(g4::launch_argmax(dy, dim0, ctx->am_val, ctx->am_idx, d_index, ctx->dev,
                                            ctx->stream), "argmax");
   }
@@ -890,7 +955,7 @@ int g4_argmax(g4_ctx *ctx, const float *v, int32_t n, int32_t *index) {
   G4_TRY(check_ctx(ctx));
   if (n <= 0) return fail(G4_ERR_INVALID_ARGUMENT, "argmax needs size > 0 (FloatTensor.kt:54)");
   if (!v || !index) return fail(G4_ERR_INVALID_ARGUMENT, "v/index is null");
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t ov = c.add(sizeof(float) * (size_t)n), oi = c.add(sizeof(int32_t));
   G4_TRY(ensure_scratch(ctx, c.off));
@@ -923,7 +988,7 @@ int g4_dequant(g4_ctx *ctx, const g4_weight *w, int64_t offset, int64_t n, float
                 (long long)(offset + n), (long long)w->n_elems);
   if (!out && n > 0) return fail(G4_ERR_INVALID_ARGUMENT, "out is null");
   if (n == 0) return ok();
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t oo = c.add(sizeof(float) * (size_t)n);
   G4_TRY(ensure_scratch(ctx, c.off));
@@ -953,7 +1018,7 @@ int g4_ffn(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, const g4
   G4_TRY(check_ctx(ctx));
   G4_TRY(check_ffn(ctx, w_gate, w_up, w_down, dim, hidden));
   if (!x || !y) return fail(G4_ERR_INVALID_ARGUMENT, "x/y is null");
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t ox = c.add(sizeof(float) * (size_t)dim), oy = c.add(sizeof(float) * (size_t)dim),
          oh = c.add(sizeof(float) * (size_t)hidden), og = c.add(sizeof(float) * 2 * (size_t)hidden);
@@ -984,7 +1049,7 @@ int g4_ffn_gate_up(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, 
   G4_TRY(check_ctx(ctx));
   G4_TRY(check_ffn(ctx, w_gate, w_up, nullptr, dim, hidden));
   if (!x || !h) return fail(G4_ERR_INVALID_ARGUMENT, "x/h is null");
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t ox = c.add(sizeof(float) * (size_t)dim), oh = c.add(sizeof(float) * (size_t)hidden),
          og = c.add(sizeof(float) * 2 * (size_t)hidden);
@@ -1030,7 +1095,7 @@ int g4_moe_route(g4_ctx *ctx, const float *logits, int32_t T, int32_t n_experts,
   G4_TRY(check_route(T, n_experts, k));
   if (T == 0 || k == 0) return ok();
   if (!logits || !ids || !weights) return fail(G4_ERR_INVALID_ARGUMENT, "logits/ids/weights is null");
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t ol = c.add(sizeof(float) * (size_t)T * n_experts), os = c.add(sizeof(float) * (size_t)n_experts),
          oi = c.add(sizeof(int32_t) * (size_t)T * k), ow = c.add(sizeof(float) * (size_t)T * k);
@@ -1069,7 +1134,7 @@ int g4_moe(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, con
   for (int64_t i = 0; i < (int64_t)T * k; ++i)
     if (ids[i] < 0 || ids[i] >= ne)
       return fail(G4_ERR_OUT_OF_RANGE, "expert id %d at %lld outside 0..%d", ids[i], (long long)i, ne - 1);
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t ox = c.add(sizeof(float) * (size_t)T * dim), oi = c.add(sizeof(int32_t) * (size_t)T * k),
          ow = c.add(sizeof(float) * (size_t)T * k), oy = c.add(sizeof(float) * (size_t)T * dim);
@@ -1127,7 +1192,7 @@ int g4_moe_routed(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_do
   if (T == 0) return ok();
   if (!X || !Y || !logits || (k > 0 && (!ids || !weights)))
     return fail(G4_ERR_INVALID_ARGUMENT, "X/Y/logits/ids/weights is null");
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t ox = c.add(sizeof(float) * (size_t)T * dim), ol = c.add(sizeof(float) * (size_t)T * n_experts),
          os = c.add(sizeof(float) * (size_t)n_experts), oi = c.add(sizeof(int32_t) * (size_t)T * k),
@@ -1238,7 +1303,7 @@ int g4_matmul_norm_dev(g4_ctx *ctx, const g4_weight *w, int64_t this_offset, con
     return fail(G4_ERR_INVALID_ARGUMENT, "xnorm overlaps x");
   G4_TRY(use_device(ctx));
   if (dim1 == 0) {
-    if (dim0 > 0) G4_HIP(hipMemsetAsync(d_out, 0, sizeof(float) * (size_t)dim0, ctx->stream), "hipMemsetAsync");
+    if (dim0 > 0) G4_TRY(zero_dev(ctx, d_out, sizeof(float) * (size_t)dim0));
     return ok();
   }
   if (dim0 == 0) {
@@ -1265,7 +1330,7 @@ int g4_ffn_block(g4_ctx *ctx, const g4_weight *w_gate, const g4_weight *w_up, co
   G4_TRY(check_ctx(ctx));
   G4_TRY(check_ffn_block(ctx, w_gate, w_up, w_down, norm_pre, norm_post, dim, hidden, eps));
   if (!x) return fail(G4_ERR_INVALID_ARGUMENT, "x is null");
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t ox = c.add(sizeof(float) * (size_t)dim), oh, oy, og, on;
   ffn_block_scratch(w_gate, dim, hidden, c, &oh, &oy, &og, &on);
@@ -1299,7 +1364,7 @@ int g4_lm_head(g4_ctx *ctx, const g4_weight *w_cls, const g4_weight *norm_final,
   G4_TRY(check_ctx(ctx));
   G4_TRY(check_lm_head(ctx, w_cls, norm_final, vocab, dim, eps, softcap));
   if (!x || !index) return fail(G4_ERR_INVALID_ARGUMENT, "x/index is null");
-  G4_TRY(use_device(ctx));
+  G4_TRY(use_host(ctx));
   Carve c;
   size_t ox = c.add(sizeof(float) * (size_t)dim), on = c.add(sizeof(float) * (size_t)dim),
          oy = c.add(sizeof(float) * (size_t)vocab), oi = c.add(sizeof(int32_t));

@@ -26,6 +26,20 @@ G4_DEV uint32_t opaque(uint32_t v) {
   return v;
 }
 
+// A value rounded to its type and materialised: no fused multiply-add is formed
+// across it.  HIP's __fmul_rn / __fadd_rn are plain operators here, and the
+// compiler's default contraction (-ffp-contract=fast-honor-pragmas) would fuse
+// a*b + c into one rounding where the reference (the JVM, which never fuses)
+// rounds the product first.
+G4_DEV float rounded(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+G4_DEV double rounded(double v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // binary16 -> binary32 (v_cvt_f32_f16; fp16 denormals are preserved in the
 // kernels' default float mode, so this is the exact decode of
 // FloatTensorHelpers.kt:39-41).
@@ -60,7 +74,10 @@ G4_DEV int q4k_scale_min(int j, const uint8_t *s, bool is_min) {
 // Q8_0FloatTensor.kt:21-28, Q4_0FloatTensor.kt:21-39, Q4_KFloatTensor.kt:23-55,
 // Q5_KFloatTensor.kt:23-50, Q6_KFloatTensor.kt:26-75, F16FloatTensor.kt:20-23,
 // BF16FloatTensor.kt:20-24, F32FloatTensor.kt:18-20.
-// __fmul_rn/__fsub_rn keep each operation separately rounded like the JVM.
+// Every product here is exact in fp32 (at most 11 + 8 significant bits, or d*sc
+// then *q within 24) or a chain of products, and the one subtraction takes an
+// exact dmin*m, so each result is the reference's bit for bit however the
+// compiler contracts.
 template <int TYPE>
 G4_DEV float get_elem(const uint8_t *W, int64_t idx) {
   if constexpr (TYPE == T_Q8_0) {
@@ -179,9 +196,13 @@ struct FmtQ8_0 {
 // block is the low nibble of byte k, element 16 + k the high nibble; value
 // (q - 8) * d (Q4_0FloatTensor.kt:21-39).  The high nibble is used in place
 // (16 q, exact) and the 1/16 folded into the block sum; -8 enters through the
-// precomputed sum of x.
+// precomputed sums of x over each 16 elements.  Those sums run in the same
+// order as the weighted sums they are taken from (x[0], x[1], ... from 0), so
+// a half block of q = 8 -- weights that are exactly zero, as the reference
+// forms them (q - 8 before the product, Q4_0FloatTensor.kt:80-81) -- cancels
+// to exactly 0: 8 * x and 128 * x are exact and scale every rounding with them.
 struct FmtQ4_0 {
-  static constexpr int TYPE = T_Q4_0, NDW = 9, NS = 2, RT = 2;
+  static constexpr int TYPE = T_Q4_0, NDW = 9, NS = 4, RT = 2;
   G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
     const uint8_t *p = W + (e >> 6) * 36;
     const u32x4a4 *v = (const u32x4a4 *)p;
@@ -191,12 +212,16 @@ struct FmtQ4_0 {
     D[8] = ((const uint32_t *)p)[8];
   }
   G4_DEV static void sums(const float *x, float *s) {
-    float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) s0 += x[k], s1 += x[32 + k];
-    s[0] = s0; s[1] = s1;
+    for (int k = 0; k < 4; ++k) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) t += x[16 * k + i];
+      s[k] = t;
+    }
   }
-  G4_DEV static float block(const uint32_t (&Q)[4], const float *x, float sx) {
+  // sl / sh: the sums of x over the block's low / high 16 elements
+  G4_DEV static float block(const uint32_t (&Q)[4], const float *x, float sl, float sh) {
     float lo = 0.f, hi = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -207,7 +232,7 @@ struct FmtQ4_0 {
         hi = __builtin_fmaf(x[16 + 4 * i + b], ubyte(h, b), hi);
       }
     }
-    return __builtin_fmaf(-8.f, sx, __builtin_fmaf(hi, 0.0625f, lo));
+    return __builtin_fmaf(__builtin_fmaf(-128.f, sh, hi), 0.0625f, __builtin_fmaf(-8.f, sl, lo));
   }
   G4_DEV static float dot(const uint32_t (&D)[NDW], const float *x, const float *s, int64_t e) {
     (void)e;
@@ -217,8 +242,8 @@ struct FmtQ4_0 {
       Q0[i] = __builtin_amdgcn_alignbyte(D[i + 1], D[i], 2);  // bytes 2..17
       Q1[i] = D[5 + i];                                          // bytes 20..35
     }
-    float t0 = block(Q0, x, s[0]);
-    float t1 = block(Q1, x + 32, s[1]);
+    float t0 = block(Q0, x, s[0], s[1]);
+    float t1 = block(Q1, x + 32, s[2], s[3]);
     return __builtin_fmaf(h2f(D[0] & 0xFFFFu), t0, h2f(D[4] >> 16) * t1);
   }
 };
@@ -226,7 +251,10 @@ struct FmtQ4_0 {
 // Q4_K: super-block {fp16 d, fp16 dmin, scales[12], qs[128]} (144 B).  Group g
 // (64 weights) uses qs[32g .. 32g+32): low nibbles are sub-block 2g, high
 // nibbles sub-block 2g+1; w = d*sc*q - dmin*m (Q4_KFloatTensor.kt:23-55).
-// Per sub-block: d*sc * sum(x q) - dmin*m * sum(x).
+// Per sub-block: d*sc * sum(x q) - dmin*m * sum(x), each product rounded on its
+// own.  sum(x) runs in the order of sum(x q), so a sub-block whose weights the
+// reference forms as exactly zero (fma(q, d*sc, -dmin*m) = 0, Q4_KFloatTensor.kt:
+// 143-148, i.e. d*sc*q = dmin*m for every q in it) gives exactly 0 here too.
 struct FmtQ4_K {
   static constexpr int TYPE = T_Q4_K, NDW = 12, NS = 2, RT = 2;
   G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
@@ -271,8 +299,11 @@ struct FmtQ4_K {
     const float d = h2f(D[8] & 0xFFFFu), dmin = h2f(D[8] >> 16);
     const float d1 = d * ubyte(scp, 0), d2 = d * ubyte(scp, 1) * 0.0625f;
     const float m1 = dmin * ubyte(mp, 0), m2 = dmin * ubyte(mp, 1);
-    float r = __builtin_fmaf(d1, lo, -(m1 * s[0]));
-    return __builtin_fmaf(d2, hi, __builtin_fmaf(-m2, s[1], r));
+    return k_subblocks(d1, lo, m1, s[0], d2, hi, m2, s[1]);
+  }
+  // (d1 lo - m1 s0) + (d2 hi - m2 s1), every product and difference rounded once
+  G4_DEV static float k_subblocks(float d1, float lo, float m1, float s0, float d2, float hi, float m2, float s1) {
+    return (rounded(d1 * lo) - rounded(m1 * s0)) + (rounded(d2 * hi) - rounded(m2 * s1));
   }
 };
 
@@ -280,7 +311,7 @@ struct FmtQ4_K {
 // 16-byte aligned).  Group g as Q4_K, with the fifth bit of weight l of
 // sub-block s = 2g + h in bit s of qh[l]: q = nibble + 16 bit, w = d*sc*q -
 // dmin*m (Q5_KFloatTensor.kt:23-50).  Per sub-block: d*sc * sum(x q) -
-// dmin*m * sum(x).
+// dmin*m * sum(x), rounded as for Q4_K (exactly 0 where every weight is).
 struct FmtQ5_K {
   static constexpr int TYPE = T_Q5_K, NDW = 20, NS = 2, RT = 2;
   G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
@@ -327,8 +358,7 @@ struct FmtQ5_K {
     const float d = h2f(D[16] & 0xFFFFu), dmin = h2f(D[16] >> 16);
     const float d1 = d * ubyte(scp, 0), d2 = d * ubyte(scp, 1);
     const float m1 = dmin * ubyte(mp, 0), m2 = dmin * ubyte(mp, 1);
-    float r = __builtin_fmaf(d1, lo, -(m1 * s[0]));
-    return __builtin_fmaf(d2, hi, __builtin_fmaf(-m2, s[1], r));
+    return FmtQ4_K::k_subblocks(d1, lo, m1, s[0], d2, hi, m2, s[1]);
   }
 };
 
@@ -612,7 +642,7 @@ G4_DEV double tanh_fdlibm(double x) {
 // Llama.kt:23-25 gelu, evaluated in double like the reference.
 G4_DEV float gelu_ref(float xf) {
   double x = (double)xf;
-  double inner = 0.7978845608028654 * (x + 0.044715 * (x * x * x));
+  double inner = 0.7978845608028654 * (x + rounded(0.044715 * (x * x * x)));
   return (float)(0.5 * x * (1.0 + tanh_fdlibm(inner)));
 }
 
@@ -624,9 +654,9 @@ G4_DEV float gelu_ref(float xf) {
 enum : int { NORM_WEIGHT_AFTER = 0, NORM_WEIGHT_FIRST = 1, NORM_NO_WEIGHT = 2 };
 
 G4_DEV float norm_apply(int form, float w, float s, float x) {
-  if (form == NORM_WEIGHT_AFTER) return __fmul_rn(w, __fmul_rn(s, x));
-  if (form == NORM_WEIGHT_FIRST) return __fmul_rn(__fmul_rn(w, s), x);
-  return __fmul_rn(s, x);
+  if (form == NORM_WEIGHT_AFTER) return rounded(w * (s * x));
+  if (form == NORM_WEIGHT_FIRST) return rounded((w * s) * x);
+  return rounded(s * x);
 }
 
 // ss = fp32 sum of squares -> s = (float)(1.0 / sqrt((double)(ss / size + eps))),

@@ -111,6 +111,8 @@ hipError_t launch_moe_down(int type, const RowsArgs &a, const float *gw, int32_t
                            hipStream_t s);
 // dst = src for `bytes` (a multiple of 4; both ends 16-byte aligned), by a kernel.
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
+// dst[0 .. bytes) = 0 by a kernel (any alignment and size).
+hipError_t launch_zero(void *dst, size_t bytes, hipStream_t s);
 hipError_t launch_moe_combine(const float *ys, const float *weights, int32_t T, int32_t k, int32_t dim, float *Y,
                               hipStream_t stream);
 

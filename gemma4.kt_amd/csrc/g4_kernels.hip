@@ -792,7 +792,7 @@ __global__ __launch_bounds__(256) void k_moe_down(RowsArgs a, const float *gw, i
   __syncthreads();
   if (tid < TR && row0 + tid < a.rows) {
     float out = 0.f;
-    for (int j = 0; j < K; ++j) out = __fadd_rn(__fmul_rn(w_slot[j], cb[j][tid]), out);
+    for (int j = 0; j < K; ++j) out = rounded(w_slot[j] * cb[j][tid]) + out;
     a.y[(int64_t)tok * a.y_stride + row0 + tid] = out;
   }
 }
@@ -815,7 +815,7 @@ __global__ void k_moe_combine(const float *ys, const float *w, int32_t T, int32_
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        if (j0 + u < K) out = __fadd_rn(__fmul_rn(a[u], v[u]), out);
+        if (j0 + u < K) out = rounded(a[u] * v[u]) + out;
     }
     Y[i] = out;
   }
@@ -1277,6 +1277,20 @@ hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s) 
   if (blocks > 256) blocks = 256;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(k_copy, dim3((unsigned)blocks), dim3(256), 0, s, (uint32_t *)dst, (const uint32_t *)src, words);
+  return hipGetLastError();
+}
+
+// dst[0 .. bytes) = 0, bytewise (the degenerate-shape outputs it serves are small).
+__global__ __launch_bounds__(256) void k_zero(uint8_t *dst, int64_t bytes) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < bytes; i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = 0;
+}
+
+hipError_t launch_zero(void *dst, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return hipSuccess;
+  int64_t blocks = ((int64_t)bytes + 255) / 256;
+  if (blocks > 1024) blocks = 1024;
+  hipLaunchKernelGGL(k_zero, dim3((unsigned)blocks), dim3(256), 0, s, (uint8_t *)dst, (int64_t)bytes);
   return hipGetLastError();
 }
 

@@ -6,9 +6,14 @@
 // Exactness.  The matrix cores multiply bf16 operands into fp32 sums, and both
 // operands here are exact in bf16:
 //   * weights: a Q4_K weight is d*sc*q - dmin*m with q in 0..15 per 32-weight
-//     sub-block; q (or 16 q for the high nibbles) is an exact bf16 and the
-//     sub-block's d*sc and dmin*m are applied in fp32 after the product, as
-//     d*sc * sum(q x) - dmin*m * sum(x) (the row engine's factorisation);
+//     sub-block, written here as (d*sc/16) * 16(q - 8) + (8 d*sc - dmin*m):
+//     16(q - 8) in -128..112 is an exact bf16, and the sub-block's two fp32
+//     coefficients are applied after the products, as
+//     (d*sc/16) * sum(16(q - 8) x) + (8 d*sc - dmin*m) * sum(x).  8 d*sc is
+//     exact, so a sub-block whose weights are all exactly zero (q = 8 and
+//     8 d*sc = dmin*m) contributes exactly 0, as in the reference, whose
+//     fma(q, d*sc, -dmin*m) forms each weight first (Q4_KFloatTensor.kt:143-148);
+//     and the rounding of the sums scales with |q - 8| rather than with q;
 //   * activations: an fp32 x has 24 significant bits and splits exactly into
 //     x1 + x2 + x3, three round-to-nearest bf16 parts of 8 bits each, so three
 //     MFMAs give sum(q x) with exact products and fp32 accumulation.
@@ -55,14 +60,17 @@ G4_DEV void split3(const float (&v)[8], bf16x8 &p1, bf16x8 &p2, bf16x8 &p3) {
   }
 }
 
-// bf16 of the 8 nibble values of one K-slice: low nibbles give q, high nibbles
-// (masked in place) give 16 q; both exact.
-G4_DEV bf16x8 nibbles_bf16(uint32_t w0, uint32_t w1) {
+// bf16 of 16(q - 8) for the 8 nibbles of one K-slice.  A nibble q moved to the
+// top of its byte and xored with 0x80 is the signed byte 16(q - 8); it converts
+// to float with one sign-extending byte select and to bf16 exactly.
+G4_DEV uint32_t lo_nibbles_s16(uint32_t w) { return ((w << 4) & 0xF0F0F0F0u) ^ 0x80808080u; }
+G4_DEV uint32_t hi_nibbles_s16(uint32_t w) { return (w & 0xF0F0F0F0u) ^ 0x80808080u; }
+G4_DEV bf16x8 nibbles_bf16(uint32_t v0, uint32_t v1) {
   bf16x8 r;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    r[b] = (__bf16)ubyte(w0, b);
-    r[4 + b] = (__bf16)ubyte(w1, b);
+    r[b] = (__bf16)sbyte(v0, b);
+    r[4 + b] = (__bf16)sbyte(v1, b);
   }
   return r;
 }
@@ -175,8 +183,8 @@ __global__ __launch_bounds__(512) void k_tok_q4k(TokArgs a) {
     for (int gi = 0; gi < GPW; ++gi) {
       if (gi < ng) {  // wave-uniform
         const uint32_t w0 = Q[gi].x, w1 = Q[gi].y;
-        const bf16x8 bl = nibbles_bf16(opaque(w0 & 0x0F0F0F0Fu), opaque(w1 & 0x0F0F0F0Fu));
-        const bf16x8 bh = nibbles_bf16(opaque(w0 & 0xF0F0F0F0u), opaque(w1 & 0xF0F0F0F0u));
+        const bf16x8 bl = nibbles_bf16(opaque(lo_nibbles_s16(w0)), opaque(lo_nibbles_s16(w1)));
+        const bf16x8 bh = nibbles_bf16(opaque(hi_nibbles_s16(w0)), opaque(hi_nibbles_s16(w1)));
         // getScaleMinK4 (Q4_KFloatTensor.kt:70-84) for sub-blocks 2g, 2g+1 of
         // this lane's row: bytes 2(g&1), 2(g&1)+1 of the three scale dwords
         const int g = gs[gi];
@@ -185,8 +193,10 @@ __global__ __launch_bounds__(512) void k_tok_q4k(TokArgs a) {
         const uint32_t scp = g < 2 ? (y & 0x3F3Fu) : ((w & 0x0F0Fu) | ((y >> 2) & 0x3030u));
         const uint32_t mp = g < 2 ? (z & 0x3F3Fu) : (((w >> 4) & 0x0F0Fu) | ((z >> 2) & 0x3030u));
         const float d = h2f(H[gi].x & 0xFFFFu), dmin = h2f(H[gi].x >> 16);
-        const float d1 = d * ubyte(scp, 0), d2 = d * ubyte(scp, 1) * 0.0625f;
-        const float m1 = dmin * ubyte(mp, 0), m2 = dmin * ubyte(mp, 1);
+        const float ds1 = d * ubyte(scp, 0), ds2 = d * ubyte(scp, 1);  // exact (11 x 6 bits)
+        const float d1 = ds1 * 0.0625f, d2 = ds2 * 0.0625f;
+        const float c1 = __builtin_fmaf(8.f, ds1, -(dmin * ubyte(mp, 0)));
+        const float c2 = __builtin_fmaf(8.f, ds2, -(dmin * ubyte(mp, 1)));
         // every token tile's products first, then the scale epilogues: the
         // matrix core works through the independent chains while they drain
         f32x4 pl[TT], ph[TT];
@@ -205,8 +215,8 @@ __global__ __launch_bounds__(512) void k_tok_q4k(TokArgs a) {
           for (int i = 0; i < 4; ++i) {
             acc[ti][i] = __builtin_fmaf(d1, pl[ti][i], acc[ti][i]);
             acc[ti][i] = __builtin_fmaf(d2, ph[ti][i], acc[ti][i]);
-            acc[ti][i] = __builtin_fmaf(-m1, xs[ti][gi][0][i], acc[ti][i]);
-            acc[ti][i] = __builtin_fmaf(-m2, xs[ti][gi][1][i], acc[ti][i]);
+            acc[ti][i] = __builtin_fmaf(c1, xs[ti][gi][0][i], acc[ti][i]);
+            acc[ti][i] = __builtin_fmaf(c2, xs[ti][gi][1][i], acc[ti][i]);
           }
       }
     }

@@ -85,6 +85,8 @@ SIGNATURES = {
     "g4_ctx_set_stream": [_vp, _vp],
     "g4_ctx_sync": [_vp],
     "g4_ctx_device": [_vp, _c_i32p],
+    "g4_ctx_reserve": [_vp, _i64],
+    "g4_ctx_scratch_bytes": [_vp, ctypes.POINTER(_i64)],
     "g4_upload": [_vp, ctypes.c_int, _vp, _i64, _i64, ctypes.POINTER(_vp)],
     "g4_weight_free": [_vp],
     "g4_weight_info": [_vp, _c_i32p, ctypes.POINTER(_i64), ctypes.POINTER(_i64)],
@@ -272,6 +274,15 @@ class Context:
 
     def sync(self) -> None:
         check(lib().g4_ctx_sync(self.handle))
+
+    def reserve(self, nbytes: int) -> None:
+        """Grow the context's device scratch now (before a HIP graph capture)."""
+        check(lib().g4_ctx_reserve(self.handle, int(nbytes)))
+
+    def scratch_bytes(self) -> int:
+        v = _i64()
+        check(lib().g4_ctx_scratch_bytes(self.handle, ctypes.byref(v)))
+        return v.value
 
     def close(self) -> None:
         if self.handle:

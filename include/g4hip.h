@@ -79,6 +79,20 @@ int g4_close(g4_ctx *ctx);
 int g4_ctx_set_stream(g4_ctx *ctx, void *stream);
 int g4_ctx_sync(g4_ctx *ctx);
 int g4_ctx_device(const g4_ctx *ctx, int *ordinal);
+/* Scratch for HIP graph capture.  *_dev calls keep intermediates (MoE hidden
+ * vectors, attention and column-split partials, a standalone norm) in a
+ * per-context device buffer that grows on demand.  A graph captured over such a
+ * call keeps that buffer's address, so:
+ *  - g4_ctx_reserve grows the buffer to `bytes` now (call it, or run the largest
+ *    shapes once eagerly, before capturing);
+ *  - a call that needs more than is reserved while its stream is capturing
+ *    returns G4_ERR_INVALID_ARGUMENT and records nothing;
+ *  - once any call on the context has been captured, an outgrown buffer is kept
+ *    allocated (graphs may still replay into it) until g4_close.
+ * Host-pointer calls synchronise and return G4_ERR_INVALID_ARGUMENT under capture.
+ * No counterpart in the reference (its matmul is synchronous CPU code). */
+int g4_ctx_reserve(g4_ctx *ctx, int64_t bytes);
+int g4_ctx_scratch_bytes(const g4_ctx *ctx, int64_t *bytes);
 
 /* FloatTensorFactory.kt:7-23 create(ggmlType, entry) + the GGUF slice of
  * GGUF.kt:195-212: copy `nbytes` raw GGUF bytes holding `n_elems` elements to HBM.
