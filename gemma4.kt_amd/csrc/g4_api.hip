@@ -9,6 +9,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -58,7 +59,19 @@ struct g4_weight {
   uint8_t *d;
 };
 
+// Scratch of g4_moe_routed_dev_noalloc: a fixed device array, one copy per GPU
+// that loads the library, held until the process ends.  Host code never uses
+// the array's name as an address (on the host it is only a stand-in): each
+// device's own address comes from hipGetSymbolAddress in g4_open and is kept in
+// g_noalloc_scratch.
+constexpr size_t G4_NOALLOC_SCRATCH_BYTES = size_t(16) << 20;
+static __device__ __align__(256) unsigned char noalloc_scratch[G4_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int G4_MAX_DEVICES = 64;
+std::mutex g_noalloc_mu;
+char *g_noalloc_scratch[G4_MAX_DEVICES];  // device address of noalloc_scratch per ordinal
 
 thread_local std::string g_last_error;
 
@@ -698,6 +711,21 @@ int g4_open(int ordinal, g4_ctx **out) {
     return hip_fail(e, "hipStreamCreate");
   }
   c->stream = c->own_stream;
+  if (ordinal < G4_MAX_DEVICES) {
+    // once per device, with the device current: the address of its copy of the
+    // allocation-free entry point's scratch
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_scratch[ordinal]) {
+      void *sp = nullptr;
+      e = hipGetSymbolAddress(&sp, HIP_SYMBOL(noalloc_scratch));
+      if (e != hipSuccess) {
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return hip_fail(e, "hipGetSymbolAddress(noalloc_scratch)");
+      }
+      g_noalloc_scratch[ordinal] = (char *)sp;
+    }
+  }
   const int nb = g4::max_argmax_blocks(c->dev);
   void *p = nullptr;
   size_t bytes = up(sizeof(float) * nb) + up(sizeof(int32_t) * nb) + up(sizeof(int32_t));
@@ -1233,6 +1261,34 @@ int g4_moe_routed_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *
   moe_scratch(T, dim, ff, k, c, &oh, &oys, &ogu);
   G4_TRY(ensure_scratch(ctx, c.off));
   char *s = ctx->scratch;
+  const MoeRoute route = {d_logits, n_experts, renormalize, d_expert_scale};
+  return moe_dev(ctx, w_gate_up, w_down, ne, d_X, T, dim, ff, d_ids, d_weights, k, d_Y, (float *)(s + oh),
+                 (float *)(s + oys), (float *)(s + ogu), &route);
+}
+
+int g4_moe_routed_dev_noalloc(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *d_X,
+                              int32_t T, int32_t dim, int32_t ff, const float *d_logits, int32_t n_experts, int32_t k,
+                              int32_t renormalize, const float *d_expert_scale, int32_t *d_ids, float *d_weights,
+                              float *d_Y) {
+  G4_TRY(check_ctx(ctx));
+  int32_t ne = 0;
+  G4_TRY(check_moe(ctx, w_gate_up, w_down, T, dim, ff, k, &ne));
+  G4_TRY(check_moe_routed(ne, n_experts, k));
+  if (T == 0) return ok();
+  if (!d_X || !d_Y || !d_logits || (k > 0 && (!d_ids || !d_weights)))
+    return fail(G4_ERR_INVALID_ARGUMENT, "X/Y/logits/ids/weights is null");
+  Carve c;
+  size_t oh, oys, ogu;
+  moe_scratch(T, dim, ff, k, c, &oh, &oys, &ogu);
+  if (c.off > G4_NOALLOC_SCRATCH_BYTES)
+    return fail(G4_ERR_INVALID_ARGUMENT,
+                "%d tokens x %d slots need %zu bytes of scratch (4 * T * k * (3 * ff + dim), rounded up); "
+                "the allocation-free entry point holds %zu",
+                T, k, c.off, G4_NOALLOC_SCRATCH_BYTES);
+  if (ctx->device >= G4_MAX_DEVICES || !g_noalloc_scratch[ctx->device])
+    return fail(G4_ERR_DEVICE, "no static scratch for device %d", ctx->device);
+  G4_TRY(use_device(ctx));
+  char *s = g_noalloc_scratch[ctx->device];
   const MoeRoute route = {d_logits, n_experts, renormalize, d_expert_scale};
   return moe_dev(ctx, w_gate_up, w_down, ne, d_X, T, dim, ff, d_ids, d_weights, k, d_Y, (float *)(s + oh),
                  (float *)(s + oys), (float *)(s + ogu), &route);

@@ -111,6 +111,7 @@ SIGNATURES = {
     "g4_moe_dev": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp],
     "g4_moe_routed": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp],
     "g4_moe_routed_dev": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp],
+    "g4_moe_routed_dev_noalloc": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp],
     "g4_rmsnorm_dev": [_vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, ctypes.c_int],
     "g4_rmsnorm_add_dev": [_vp, _vp, _vp, _vp, _i32, ctypes.c_float],
     "g4_add_dev": [_vp, _vp, _vp, _i32],
@@ -548,6 +549,17 @@ def moe_routed_dev(ctx: Context, gate_up, down, X, T: int, dim: int, ff: int, lo
                                   int(bool(renormalize)), _ptr(_dev_f32(expert_scale, "expert_scale")),
                                   _ptr(_dev_i32(ids, "ids")),
                                   _ptr(_dev_f32(weights, "weights")), _ptr(_dev_f32(Y, "Y"))))
+
+
+def moe_routed_dev_noalloc(ctx: Context, gate_up, down, X, T: int, dim: int, ff: int, logits, n_experts: int, k: int,
+                           renormalize: bool, ids, weights, Y, expert_scale=None) -> None:
+    """moe_routed_dev with its intermediates in the library's fixed per-GPU scratch
+    (no device allocation; calls overlapping on one GPU race)."""
+    check(lib().g4_moe_routed_dev_noalloc(ctx.handle, gate_up.handle, down.handle, _ptr(_dev_f32(X, "X")), int(T),
+                                          int(dim), int(ff), _ptr(_dev_f32(logits, "logits")), int(n_experts), int(k),
+                                          int(bool(renormalize)), _ptr(_dev_f32(expert_scale, "expert_scale")),
+                                          _ptr(_dev_i32(ids, "ids")), _ptr(_dev_f32(weights, "weights")),
+                                          _ptr(_dev_f32(Y, "Y"))))
 
 
 # ------------------------------------------------------------ decode step ---

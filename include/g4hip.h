@@ -188,6 +188,20 @@ int g4_moe_routed_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *
                       int32_t renormalize, const float *d_expert_scale, int32_t *d_ids, float *d_weights,
                       float *d_Y);
 
+/* g4_moe_routed_dev without any device allocation, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Same arguments, results
+ * and bits as g4_moe_routed_dev; its intermediates live in a fixed 16 MiB device
+ * array per GPU (held until the process ends) instead of the context's scratch,
+ * so 4 * T * k * (3 * ff + dim) bytes (each part rounded up to 256) must fit:
+ * larger calls return G4_ERR_INVALID_ARGUMENT.  Every call on one GPU shares
+ * that array: calls that overlap on one GPU (other threads, other streams or
+ * contexts) race and must be serialised by the caller. */
+int g4_moe_routed_dev_noalloc(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *d_X,
+                              int32_t T, int32_t dim, int32_t ff, const float *d_logits, int32_t n_experts, int32_t k,
+                              int32_t renormalize, const float *d_expert_scale, int32_t *d_ids, float *d_weights,
+                              float *d_Y);
+
 /* ---- Decode step around the matvec: the activations stay in device memory. ----
  * Norm weights are uploaded F32 tensors (ModelLoader.kt:281-286 reads norms as
  * FloatBuffers and throws UnsupportedOperationException for any other type).
