@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libg4hip.so")
-SOURCES = ["g4_api.hip", "g4_kernels.hip", "g4_tok.hip", "g4_attn.hip"]
+SOURCES = ["g4_api.hip", "g4_kernels.hip", "g4_tok.hip", "g4_attn.hip", "g4_wide.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 # Packed fp32 VALU ops are disabled on purpose: every fp32 op stays scalar-rounded.

@@ -98,6 +98,12 @@ bool tok_ok(int type, const TokArgs &a);
 int64_t tok_scratch_floats(const TokArgs &a, const DevInfo &dev);
 hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_t stream);
 
+// Plain matvec of rows of 65..256 chunks (g4_wide.hip): the columns split over
+// the waves of a workgroup.  wide_ok: the launch takes it (EPI_STORE, no ids,
+// no fused norm or routing, 64-element aligned rows of the row-stream formats).
+bool wide_ok(int type, const RowsArgs &a, int epi);
+hipError_t launch_wide(int type, const RowsArgs &a, int segments, hipStream_t stream);
+
 hipError_t launch_dequant(int type, const uint8_t *W, int64_t offset, int64_t n, float *out, hipStream_t stream);
 hipError_t launch_argmax(const float *v, int32_t n, float *part_val, int32_t *part_idx, int32_t *out,
                          const DevInfo &dev, hipStream_t stream);

@@ -1105,6 +1105,7 @@ hipError_t launch_rows(int type, int epi, const RowsArgs &a, int segments, const
       return launch_rows(type, epi, b, segments, dev, scratch, s);
     }
   }
+  if (wide_ok(type, a, epi)) return launch_wide(type, a, segments, s);
   if (rows_fast_ok(type, a, epi == EPI_GELU_PAIR)) {
     switch (type) {
       case T_Q8_0: return launch_fast<FmtQ8_0>(epi, a, segments, dev, s);
