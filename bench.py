@@ -702,6 +702,11 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool,
                       file=sys.stderr)
                 step_graph = None
                 torch.cuda.synchronize()
+        # each launch of a step timed on its own (the roofline figures), before the
+        # timed region: the GPU then runs the timed steps warm, as a decode loop does
+        # (the first replays over a large working set, such as the 623 MB of MoE
+        # experts, run up to 25% slower)
+        parts = _time_parts(wl, ctx, stream, torch, copies, use_graph, capture)
         ctx.set_stream(stream.cuda_stream)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -714,7 +719,6 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool,
         elapsed = time.perf_counter() - t0
         graphed = step_graph is not None
         del step_graph
-        parts = _time_parts(wl, ctx, stream, torch, copies, use_graph, capture)
         ctx.set_stream(None)
     # the host-pointer entry point of the same step (copies in and out, synchronous;
     # not part of `value`): after a few untimed calls, the mean over whole passes
