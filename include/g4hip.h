@@ -167,7 +167,11 @@ int g4_moe_route_dev(g4_ctx *ctx, const float *d_logits, int32_t T, int32_t n_ex
  *   Y[t] = sum_j weights[t,j] * down_e( gelu(gate_e X[t]) * up_e X[t] ),  e = ids[t,j]
  * w_gate_up: [n_experts x 2*ff x dim] (gate rows first, then up rows, per expert,
  * slab offset e*2*ff*dim); w_down: [n_experts x dim x ff] (offset e*dim*ff).
- * X [T x dim], ids/weights [T x k], Y [T x dim]. */
+ * X [T x dim], ids/weights [T x k], Y [T x dim].
+ * g4_moe checks every id against the experts the weights hold
+ * (G4_ERR_OUT_OF_RANGE).  g4_moe_dev cannot (the ids are device memory): a slot
+ * whose id lies outside [0, n_experts) contributes nothing (its hidden vector
+ * and down rows are zero), so Y is the weighted sum over the valid slots. */
 int g4_moe(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *X, int32_t T,
            int32_t dim, int32_t ff, const int32_t *ids, const float *weights, int32_t k, float *Y);
 int g4_moe_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *d_X, int32_t T,
