@@ -49,21 +49,23 @@ Q8_0, Q4_0, Q4_K = 8, 2, 12
 # rocprofv3 --pmc passes over `bench.py --eager`: FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0
 # (KiB), the factors being what the counters read for a plain 256 MiB fp32 copy.
 # Recorded in profiles/hbm_traffic_fetch_write_size.md (same command and kernels).
+# "name:part" keys give the other separately timed launches of a step.
 TRAFFIC_BYTES = {
-    "q4_0_ffn_decode_token": 19200819,
-    "q8_0_matvec_2048x2048": 4625203,
-    "q8_0_lm_head_262144x2048_argmax": 572074394,
-    "q4_k_batched_8192x2048_m1": 9654067,
-    "q4_k_batched_8192x2048_m8": 10430259,
-    "q4_k_batched_8192x2048_m32": 16970547,
-    "q4_k_batched_8192x2048_m64": 32674611,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40358195,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 547822899,
-    "q5_k_matvec_8192x2048": 11759411,
-    "q6_k_matvec_8192x2048": 14136115,
-    "q4_0_ffn_block_decode_token": 29185638,
-    "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572318003,
-    "attention_decode_h16_kv8_d256_len8192": 136787149,
+    "q4_0_ffn_decode_token": 19201792,
+    "q4_0_ffn_decode_token:down": 9816960,
+    "q8_0_matvec_2048x2048": 4638592,
+    "q8_0_lm_head_262144x2048_argmax": 572108064,
+    "q4_k_batched_8192x2048_m1": 9658240,
+    "q4_k_batched_8192x2048_m8": 10442624,
+    "q4_k_batched_8192x2048_m32": 16976768,
+    "q4_k_batched_8192x2048_m64": 32674688,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40341696,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 547889632,
+    "q5_k_matvec_8192x2048": 11771776,
+    "q6_k_matvec_8192x2048": 14137088,
+    "q4_0_ffn_block_decode_token": 29116672,
+    "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572367648,
+    "attention_decode_h16_kv8_d256_len8192": 136787104,
 }
 
 
@@ -99,9 +101,9 @@ class Workload:
         """The timed region runs steps 0 .. steps-1 (workloads whose bytes differ per step adjust)."""
 
     def parts(self) -> list:
-        """(kernel name, algorithmic bytes per launch, launch fn(i)) of each launch of
-        a step that is timed on its own; by default the dominant kernel only."""
-        return [(self.dominant_name, self.dominant_bytes, self.dominant)]
+        """(kernel name, algorithmic bytes per launch, launch fn(i), traffic key) of each
+        launch of a step that is timed on its own; by default the dominant kernel only."""
+        return [(self.dominant_name, self.dominant_bytes, self.dominant, self.name)]
 
     # The same step through the host-pointer entry point (activations copied in,
     # results copied out, synchronous), timed apart from `value`; None: no such call.
@@ -117,7 +119,7 @@ class Workload:
 class FfnQ4_0(Workload):
     name = "q4_0_ffn_decode_token"
     dominant_name = "k_rows<FmtQ4_0, 32, EPI_GELU_PAIR> (gate+up fused)"
-    down_name = "k_rows<FmtQ4_0, 64, EPI_STORE> (down)"
+    down_name = "k_wide<FmtQ4_0, 32, 4, 2> (down)"
 
     def __init__(self, g4, ctx, torch):
         import synth
@@ -160,8 +162,8 @@ class FfnQ4_0(Workload):
     def parts(self):
         # the down launch: W_down, h read once, y written once
         down_bytes = self.c["down"].nbytes + 4 * self.hidden + 4 * self.dim
-        return [(self.dominant_name, self.dominant_bytes, self.dominant),
-                (self.down_name, down_bytes, self.down)]
+        return [(self.dominant_name, self.dominant_bytes, self.dominant, self.name),
+                (self.down_name, down_bytes, self.down, self.name + ":down")]
 
     def cpu_setup(self, oracle):
         self.oracle = oracle
@@ -300,13 +302,15 @@ class BatchedQ4_K(Workload):
 
 class MoeQ4_K(Workload):
     unit = "tokens/s"
-    dominant_name = ("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE> (routing + gate_up) + "
-                     "k_rows<FmtQ4_K, 32> (down) + k_moe_combine")
 
     def __init__(self, g4, ctx, torch, tokens=1, routings=32):
         import synth
         self.T = tokens
         self.name = "moe_q4_k_128x(2816x2048+2048x1408)_top8_t%d" % tokens
+        # one token: the down projection and the weighted sum share a launch
+        self.dominant_name = ("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE> (routing + gate_up) + " +
+                              ("k_moe_down<FmtQ4_K, 32> (down + weighted sum)" if tokens * 8 * 2 <= 256 else
+                               "k_rows<FmtQ4_K, 8, 3, XL> (down) + k_moe_combine"))
         base = synth.moe_q4_k(tokens)
         E, D, FF, K = base["n_experts"], base["dim"], base["ff"], base["k"]
         self.E, self.D, self.FF, self.K = E, D, FF, K
@@ -414,7 +418,7 @@ class FfnBlockQ4_0(Workload):
     the residual stream x updated in place in device memory."""
     name = "q4_0_ffn_block_decode_token"
     dominant_name = ("launch group of g4_ffn_block: k_rows<FmtQ4_0, 32, EPI_GELU_PAIR, NORM> + "
-                     "k_rows<FmtQ4_0, 64, EPI_STORE> + k_rmsnorm (residual)")
+                     "k_wide<FmtQ4_0, 32, 4, 2> + k_rmsnorm_v (residual)")
 
     def __init__(self, g4, ctx, torch):
         import synth
@@ -635,7 +639,7 @@ def _time_parts(wl, ctx, stream, torch, copies: int, use_graph: bool, capture) -
     cycling the weight copies (at least 64 launches)."""
     out = []
     reps = max(1, math.ceil(64 / copies))
-    for name, nbytes, fn in wl.parts():
+    for name, nbytes, fn, tkey in wl.parts():
         g = None
         if use_graph:
             try:
@@ -656,7 +660,7 @@ def _time_parts(wl, ctx, stream, torch, copies: int, use_graph: bool, capture) -
         torch.cuda.synchronize()
         us = ev0.elapsed_time(ev1) * 1e3 / (reps * copies)
         out.append({"kernel": name, "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3),
-                    "launches_timed": reps * copies})
+                    "launches_timed": reps * copies, "traffic": TRAFFIC_BYTES.get(tkey)})
     return out
 
 
