@@ -9,6 +9,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -70,8 +71,8 @@ static __device__ __align__(256) unsigned char noalloc_scratch[G4_NOALLOC_SCRATC
 namespace {
 
 constexpr int G4_MAX_DEVICES = 64;
-std::mutex g_noalloc_mu;
-char *g_noalloc_scratch[G4_MAX_DEVICES];  // device address of noalloc_scratch per ordinal
+std::mutex g_noalloc_mu;  // serialises the one-time lookups in g4_open
+std::atomic<char *> g_noalloc_scratch[G4_MAX_DEVICES];  // device address of noalloc_scratch per ordinal
 
 thread_local std::string g_last_error;
 
@@ -715,7 +716,7 @@ int g4_open(int ordinal, g4_ctx **out) {
     // once per device, with the device current: the address of its copy of the
     // allocation-free entry point's scratch
     std::lock_guard<std::mutex> lock(g_noalloc_mu);
-    if (!g_noalloc_scratch[ordinal]) {
+    if (!g_noalloc_scratch[ordinal].load(std::memory_order_acquire)) {
       void *sp = nullptr;
       e = hipGetSymbolAddress(&sp, HIP_SYMBOL(noalloc_scratch));
       if (e != hipSuccess) {
@@ -723,7 +724,7 @@ int g4_open(int ordinal, g4_ctx **out) {
         delete c;
         return hip_fail(e, "hipGetSymbolAddress(noalloc_scratch)");
       }
-      g_noalloc_scratch[ordinal] = (char *)sp;
+      g_noalloc_scratch[ordinal].store((char *)sp, std::memory_order_release);
     }
   }
   const int nb = g4::max_argmax_blocks(c->dev);
@@ -1285,10 +1286,9 @@ int g4_moe_routed_dev_noalloc(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_
                 "%d tokens x %d slots need %zu bytes of scratch (4 * T * k * (3 * ff + dim), rounded up); "
                 "the allocation-free entry point holds %zu",
                 T, k, c.off, G4_NOALLOC_SCRATCH_BYTES);
-  if (ctx->device >= G4_MAX_DEVICES || !g_noalloc_scratch[ctx->device])
-    return fail(G4_ERR_DEVICE, "no static scratch for device %d", ctx->device);
+  char *s = ctx->device < G4_MAX_DEVICES ? g_noalloc_scratch[ctx->device].load(std::memory_order_acquire) : nullptr;
+  if (!s) return fail(G4_ERR_DEVICE, "no static scratch for device %d", ctx->device);
   G4_TRY(use_device(ctx));
-  char *s = g_noalloc_scratch[ctx->device];
   const MoeRoute route = {d_logits, n_experts, renormalize, d_expert_scale};
   return moe_dev(ctx, w_gate_up, w_down, ne, d_X, T, dim, ff, d_ids, d_weights, k, d_Y, (float *)(s + oh),
                  (float *)(s + oys), (float *)(s + ogu), &route);
