@@ -22,16 +22,15 @@
 // columns), B = weight nibbles (32 columns x 16 rows), C = 16 tokens x 16 rows:
 // lane l holds A row l%16 / B column l%16 at columns 8(l/16)..+8, and C column
 // l%16 (a weight row) at tokens 4(l/16)..+4, so the lane that unpacks weight row
-// n also owns that row's outputs and scales.  A workgroup is 8 waves.  Each
-// wave keeps 4 (token tile, 64-column group) pairs of x split into bf16 parts
-// in registers -- 4 groups of one token tile, 2 groups of 2 or 1 group of 4 --
-// and walks the workgroup's 16-row tiles, unpacking each weight once for its
-// token tiles.  The 8 per-wave partial tiles are summed in wave order through
-// LDS (deterministic).  When the columns need more than one workgroup (more
-// than 8 x 4 / TT groups) the column splits store partial sums that
-// k_tok_reduce adds in split order.  Splitting the columns this way keeps the x
-// each workgroup loads and splits to its own share, so the split work does not
-// grow with the number of workgroups.
+// n also owns that row's outputs and scales.  Each wave keeps TT x GPW (token
+// tile, 64-column group) pairs of x split into bf16 parts in registers and
+// walks the workgroup's 16-row tiles, unpacking each weight once for its token
+// tiles.  The WPB per-wave partial tiles are summed in wave order through LDS
+// (deterministic).  When the columns need more than one workgroup (more than
+// WPB x GPW groups) the column splits store partial sums that k_tok_reduce
+// adds in split order.  Splitting the columns this way keeps the x each
+// workgroup loads and splits to its own share, so the split work does not grow
+// with the number of workgroups.
 #include "g4_device.hpp"
 #include "g4_internal.hpp"
 
@@ -41,8 +40,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
 
-constexpr int TOK_WAVES = 8;  // column slices (waves) per workgroup
-constexpr int TOK_SLOTS = 4;  // (token tile, 64-column group) pairs a wave keeps split in registers
+constexpr int TOK_SLOTS = 4;  // (token tile, 64-column group) pairs a wave can keep split in registers
 
 // x = p1 + p2 + p3 exactly (each residual is exact in fp32; the third has at
 // most 8 significant bits).  Infinite or NaN x stay in p1 with zero residuals.
@@ -75,19 +73,22 @@ G4_DEV bf16x8 nibbles_bf16(uint32_t v0, uint32_t v1) {
   return r;
 }
 
-// TT token tiles per wave and GPW = TOK_SLOTS / TT column groups per wave: a
-// workgroup covers TOK_WAVES * GPW groups (its column split, blockIdx.y) for TT
-// token tiles (token group blockIdx.z) over a range of 16-row tiles
-// (blockIdx.x).  A wave unpacks each weight once for its TT token tiles.
-template <int TT>
-__global__ __launch_bounds__(512) void k_tok_q4k(TokArgs a) {
-  constexpr int GPW = TOK_SLOTS / TT;
-  __shared__ f32x4 red[2][TT][TOK_WAVES][64];
+// TT token tiles and GPW column groups per wave: a workgroup of WPB waves
+// covers WPB * GPW groups (its column split, blockIdx.y) for TT token tiles
+// (token group blockIdx.z) over a range of 16-row tiles (blockIdx.x).  A wave
+// unpacks each weight once for its TT token tiles.
+// AL: base and row_stride are multiples of 256 (whole super-blocks per row, the
+// usual case): a lane's weight address then moves by a fixed stride per row
+// tile and each wave's group within the super-block is the same for all rows.
+template <int TT, int GPW, int WPB, bool AL>
+__global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
+  static_assert(TT * GPW <= TOK_SLOTS && WPB >= TT && WPB % TT == 0, "tile shape");
+  __shared__ f32x4 red[2][TT][WPB][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, j = lane >> 4;
   const int C = a.dim1 >> 6;
-  const int g0 = ((int)blockIdx.y * TOK_WAVES + wid) * GPW;  // first group of this wave's slice
+  const int g0 = ((int)blockIdx.y * WPB + wid) * GPW;  // first group of this wave's slice
   const int ng = max(0, min(GPW, C - g0));                   // wave-uniform
   const int tt0 = (int)blockIdx.z * TT;                      // first token tile
   const int n_rt = (a.rows + 15) >> 4;
@@ -100,9 +101,26 @@ __global__ __launch_bounds__(512) void k_tok_q4k(TokArgs a) {
 
   // weight group gi of row tile rt, this lane's row (B column n) and K-slice j:
   // 8 nibble bytes at qs[32 g + 8 j] and the super-block head
+  // AL: super-block of row rt0 * 16 + n and the per-tile byte stride
+  const int64_t rs_sb = a.row_stride >> 8;
+  const uint8_t *w_row0 = a.W + ((a.base >> 8) + (int64_t)(rt0 * 16 + n) * rs_sb) * 144;
+  const int64_t w_step = 16 * rs_sb * 144;
   auto load_w = [&](int rt, bool live, u32x2a4 (&Q)[GPW], u32x4 (&H)[GPW], int (&gs)[GPW]) {
     const int r = rt * 16 + n;
     const bool rok = live && r < a.rows;
+    if constexpr (AL) {
+      const uint8_t *row = w_row0 + (int64_t)(rt - rt0) * w_step;
+#pragma unroll
+      for (int gi = 0; gi < GPW; ++gi) {
+        const int g = g0 + gi;
+        // rows past the end and groups past the slice read the first super-block
+        const uint8_t *sb = (rok && gi < ng) ? row + (g >> 2) * 144 : a.W;
+        gs[gi] = g & 3;  // wave-uniform
+        H[gi] = *(const u32x4 *)sb;
+        Q[gi] = *(const u32x2a4 *)(sb + 16 + 32 * (g & 3) + 8 * j);
+      }
+      return;
+    }
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi) {
       // rows past the end and groups past the slice read the first group of
@@ -220,25 +238,23 @@ __global__ __launch_bounds__(512) void k_tok_q4k(TokArgs a) {
           }
       }
     }
-    // the TOK_WAVES column slices are summed in wave order (deterministic),
-    // the work spread over the waves: wave w takes token tile w / (8 / TT)'s
-    // components i = c, c + 8/TT, ... of every lane's 4 outputs (c = w % (8/TT))
+    // the WPB column slices are summed in wave order (deterministic), the work
+    // spread over the waves: wave w takes token tile w / (WPB / TT)'s components
+    // i = c, c + WPB/TT, ... of every lane's 4 outputs (c = w % (WPB / TT))
 #pragma unroll
     for (int ti = 0; ti < TT; ++ti) red[buf][ti][wid][lane] = acc[ti];
     __syncthreads();
     {
-      constexpr int WPT = TOK_WAVES / TT;  // waves per token tile
+      constexpr int WPT = WPB / TT;  // waves per token tile
       const int ti = wid / WPT, c = wid % WPT;
       const int r = rt * 16 + n;
+      for (int i = c; i < 4; i += WPT) {  // wave-uniform: one component per read, no selects
+        const float *rp = (const float *)&red[buf][ti][0][lane] + i;
+        float s = rp[0];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (i % WPT == c) {  // wave-uniform
-          float s = red[buf][ti][0][lane][i];
-#pragma unroll
-          for (int w = 1; w < TOK_WAVES; ++w) s += red[buf][ti][w][lane][i];
-          const int m = (tt0 + ti) * 16 + 4 * j + i;
-          if (r < a.rows && m < a.M) out[(int64_t)m * out_stride + r] = s;
-        }
+        for (int w = 1; w < WPB; ++w) s += rp[w * 64 * 4];
+        const int m = (tt0 + ti) * 16 + 4 * j + i;
+        if (r < a.rows && m < a.M) out[(int64_t)m * out_stride + r] = s;
       }
     }
     buf ^= 1;
@@ -258,30 +274,48 @@ __global__ __launch_bounds__(512) void k_tok_q4k(TokArgs a) {
 }
 
 // y[m * y_stride + r] = sum over the column splits, in split order, of their
-// partial sums; workgroup (bx, m) covers rows 256 bx .. +256 of token m.
+// partial sums.  Thread t of workgroup (bx, m) covers V consecutive rows from
+// V * (256 bx + t) of token m; the loads of up to 8 splits are all in flight
+// before the first add.
+template <int V>
 __global__ __launch_bounds__(256) void k_tok_reduce(const float *part, int splits, int32_t M, int32_t rows, float *y,
                                                     int64_t y_stride) {
-  const int r = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+  typedef float fv __attribute__((ext_vector_type(V)));
+  const int r = (blockIdx.x * 256 + threadIdx.x) * V, m = blockIdx.y;
   if (r >= rows) return;
   const int64_t n = (int64_t)M * rows, i = (int64_t)m * rows + r;
-  float s = part[i];
-  for (int k = 1; k < splits; ++k) s += part[(int64_t)k * n + i];
-  y[(int64_t)m * y_stride + r] = s;
+  fv s = *(const fv *)(part + i);
+  for (int k0 = 1; k0 < splits; k0 += 8) {
+    fv v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = *(const fv *)(part + (int64_t)min(k0 + k, splits - 1) * n + i);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k0 + k < splits) s += v[k];
+  }
+  *(fv *)(y + (int64_t)m * y_stride + r) = s;
 }
 
+// Launch shape: one 16-token tile and two 64-column groups per wave, 16
+// waves per workgroup (four per SIMD at <= 128 VGPRs), one workgroup per CU:
+// a workgroup covers 2048 columns.  Measured over 1/2/4 token tiles, 1/2/4
+// groups and 4/8/16 waves for M = 8..64 at 8192 x 2048, this shape was the
+// fastest or within 2% at every M, and it needs no column split up to 2048
+// columns.
+constexpr int TOK_TT = 1, TOK_GPW = 2, TOK_WPB = 16;
+
 struct TokShape {
-  int tt, splits, tgroups, gx;
+  int splits, tgroups, gx;
 };
 
 static TokShape tok_shape(const TokArgs &a, const DevInfo &dev) {
   TokShape sh;
   const int C = a.dim1 / 64;
   const int ntt = (a.M + 15) / 16;
-  sh.tt = ntt >= 4 ? 4 : (ntt >= 2 ? 2 : 1);
-  const int gps = TOK_WAVES * (TOK_SLOTS / sh.tt);  // groups per column split
+  const int gps = TOK_WPB * TOK_GPW;  // groups per column split
   sh.splits = (C + gps - 1) / gps;
-  sh.tgroups = (ntt + sh.tt - 1) / sh.tt;
-  // one 8-wave workgroup per CU at a time, spread over every (split, token group)
+  sh.tgroups = (ntt + TOK_TT - 1) / TOK_TT;
+  // one workgroup per CU at a time, spread over every (split, token group)
   const int n_rt = (a.rows + 15) / 16;
   int64_t gx = (int64_t)dev.cu_count / ((int64_t)sh.splits * sh.tgroups);
   if (gx > n_rt) gx = n_rt;
@@ -307,17 +341,21 @@ hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_
   const TokShape sh = tok_shape(a, dev);
   if (sh.splits > 1 && !a.part) return hipErrorInvalidValue;
   const dim3 grid((unsigned)sh.gx, (unsigned)sh.splits, (unsigned)sh.tgroups);
-  if (sh.tt == 4)
-    hipLaunchKernelGGL(k_tok_q4k<4>, grid, dim3(512), 0, s, a);
-  else if (sh.tt == 2)
-    hipLaunchKernelGGL(k_tok_q4k<2>, grid, dim3(512), 0, s, a);
+  if ((a.base % 256) == 0 && (a.row_stride % 256) == 0)
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_GPW, TOK_WPB, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
   else
-    hipLaunchKernelGGL(k_tok_q4k<1>, grid, dim3(512), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_GPW, TOK_WPB, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
   if (sh.splits == 1) return hipGetLastError();
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_tok_reduce, dim3((unsigned)((a.rows + 255) / 256), (unsigned)a.M), dim3(256), 0, s,
-                     (const float *)a.part, sh.splits, a.M, a.rows, a.y, a.y_stride);
+  // four rows per thread when every row quad and its output are 16-byte aligned
+  // (the scratch is; y depends on the caller)
+  if ((a.rows % 4) == 0 && (a.y_stride % 4) == 0 && ((uintptr_t)a.y & 15) == 0)
+    hipLaunchKernelGGL(k_tok_reduce<4>, dim3((unsigned)((a.rows / 4 + 255) / 256), (unsigned)a.M), dim3(256), 0, s,
+                       (const float *)a.part, sh.splits, a.M, a.rows, a.y, a.y_stride);
+  else
+    hipLaunchKernelGGL(k_tok_reduce<1>, dim3((unsigned)((a.rows + 255) / 256), (unsigned)a.M), dim3(256), 0, s,
+                       (const float *)a.part, sh.splits, a.M, a.rows, a.y, a.y_stride);
   return hipGetLastError();
 }
 
