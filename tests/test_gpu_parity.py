@@ -396,13 +396,14 @@ def test_q4_k_batched(g4, ctx, oracle, m):
         assert_dots(Y[i][rows], ex[rows], ab[rows], "batched m=%d row %d" % (m, i))
 
 
-# matrix-core multi-token kernel: partial row and token tiles, several column
-# splits (summed by the reduce launch), rows that start mid super-block
-# (1408 = 5.5 super-blocks), a row offset, a single 64-column group, 1/2/4 token
-# tiles per wave and several token groups (M = 48, 70)
+# matrix-core multi-token kernel (M >= 3): partial row and token tiles, several
+# column splits (summed by the reduce launch: 4224 and 4096 columns), rows that
+# start mid super-block (1408 = 5.5 super-blocks), a row offset, a single
+# 64-column group and several token groups (M = 17, 48, 70); M = 2 takes the
+# row engine, one segment per token
 @pytest.mark.parametrize("m,rows,dim1,off_rows", [
-    (2, 40, 2048, 0), (17, 34, 4224, 0), (5, 34, 1408, 0), (16, 48, 2048, 3), (3, 20, 64, 0),
-    (48, 40, 2048, 0), (70, 24, 4096, 1)])
+    (2, 40, 2048, 0), (4, 40, 2048, 0), (17, 34, 4224, 0), (5, 34, 1408, 0), (16, 48, 2048, 3),
+    (3, 20, 64, 0), (48, 40, 2048, 0), (70, 24, 4096, 1)])
 def test_q4_k_batched_matrix_core_shapes(g4, ctx, oracle, m, rows, dim1, off_rows):
     announce("q4_k batched M=%d rows=%d dim1=%d off_rows=%d" % (m, rows, dim1, off_rows))
     n = (rows + off_rows) * dim1
