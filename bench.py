@@ -54,17 +54,17 @@ TRAFFIC_BYTES = {
     "q4_0_ffn_decode_token": 19201792,
     "q4_0_ffn_decode_token:down": 9816960,
     "q8_0_matvec_2048x2048": 4638592,
-    "q8_0_lm_head_262144x2048_argmax": 572108064,
+    "q8_0_lm_head_262144x2048_argmax": 572075040,
     "q4_k_batched_8192x2048_m1": 9658240,
-    "q4_k_batched_8192x2048_m8": 10442624,
-    "q4_k_batched_8192x2048_m32": 16976768,
-    "q4_k_batched_8192x2048_m64": 32674688,
+    "q4_k_batched_8192x2048_m8": 10338048,
+    "q4_k_batched_8192x2048_m32": 12697344,
+    "q4_k_batched_8192x2048_m64": 15843072,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40341696,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 547889632,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 547372448,
     "q5_k_matvec_8192x2048": 11771776,
     "q6_k_matvec_8192x2048": 14137088,
     "q4_0_ffn_block_decode_token": 29116672,
-    "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572367648,
+    "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572359552,
     "attention_decode_h16_kv8_d256_len8192": 136787104,
 }
 
@@ -263,10 +263,11 @@ class BatchedQ4_K(Workload):
         import synth
         c = synth.q4_k_batched(m)
         self.c, self.m = c, m
-        # one token: the row-stream kernel; several: the matrix-core kernel (1, 2 or 4
-        # token tiles per wave) plus the column-split reduce when it splits columns
-        self.dominant_name = ("k_rows<FmtQ4_K, 32, EPI_STORE>" if m == 1 else
-                              "k_tok_q4k<TT> (+ k_tok_reduce), bf16x3 MFMA 16x16x32")
+        # one or two tokens: the row-stream kernel (one segment per token); three or
+        # more: the matrix-core kernel (one column split up to 2048 columns, more
+        # splits summed by k_tok_reduce)
+        self.dominant_name = ("k_rows<FmtQ4_K, 32, EPI_STORE>" if m <= 2 else
+                              "k_tok_q4k<1, 2, 16> (bf16x3 MFMA 16x16x32)")
         self.name = "q4_k_batched_8192x2048_m%d" % m
         R, D = c["dim0"], c["dim1"]
         self.R, self.D = R, D
