@@ -703,12 +703,18 @@ __global__ __launch_bounds__(256) void k_route(const float *logits, int32_t E, i
 // dim1 <= 64 * LPR.
 constexpr int MOE_DOWN_MAX_K = 8;
 
-template <class F, int LPR>
-__global__ __launch_bounds__(256) void k_moe_down(RowsArgs a, const float *gw, int32_t K) {
-  constexpr int RT = F::RT, RPW = 64 / LPR, TR = RT * RPW, NDW = F::NDW;
+// WPB waves: wave w takes slots w and w + WPB (WPB = 4: two slots; WPB = 8: one)
+// over RT = F::RT * WPB / 4 row steps, so a wave always holds 2 * F::RT chunks
+// in flight and the 8-wave shape covers twice the rows per workgroup: every
+// workgroup stages all K slots' x, so rows per workgroup set the x traffic.
+template <class F, int LPR, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_moe_down(RowsArgs a, const float *gw, int32_t K) {
+  static_assert(WPB == 4 || WPB == 8, "4 or 8 waves");
+  constexpr int NT = 64 * WPB;
+  constexpr int RT = F::RT * WPB / 4, RPW = 64 / LPR, TR = RT * RPW, NDW = F::NDW;
   constexpr int XS = LPR * 16;                          // 16-byte x segments of one slot
-  constexpr int XSEG = MOE_DOWN_MAX_K * XS / 256;       // staged by each thread
-  static_assert(XSEG * 256 == MOE_DOWN_MAX_K * XS, "x staging");
+  constexpr int XSEG = MOE_DOWN_MAX_K * XS / NT;        // staged by each thread
+  static_assert(XSEG * NT == MOE_DOWN_MAX_K * XS, "x staging");
   __shared__ u32x4 xl[MOE_DOWN_MAX_K][XS];
   __shared__ float cb[MOE_DOWN_MAX_K][TR];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -722,7 +728,7 @@ __global__ __launch_bounds__(256) void k_moe_down(RowsArgs a, const float *gw, i
   u32x4a4 xr[XSEG];
 #pragma unroll
   for (int u = 0; u < XSEG; ++u) {
-    const int g = u * 256 + tid, j = g / XS, c = (g % XS) >> 4;
+    const int g = u * NT + tid, j = g / XS, c = (g % XS) >> 4;
     const bool in = (j < K) & (c < C);
     const float *xp = a.x + (int64_t)(tok * K + (in ? j : 0)) * a.x_stride + (int64_t)(in ? c : 0) * 64;
     xr[u] = ((const u32x4a4 *)xp)[g & 15];
@@ -777,10 +783,10 @@ __global__ __launch_bounds__(256) void k_moe_down(RowsArgs a, const float *gw, i
   // both slots' weights go out before the x staging waits (one token's step:
   // 21.6 -> 21.3 us against issuing the second slot after the barrier)
   load(wid, DA, okA, EA);
-  load(wid + 4, DB, okB, EB);
+  if constexpr (WPB == 4) load(wid + 4, DB, okB, EB);
 #pragma unroll
   for (int u = 0; u < XSEG; ++u) {
-    const int g = u * 256 + tid, j = g / XS, c = (g % XS) >> 4;
+    const int g = u * NT + tid, j = g / XS, c = (g % XS) >> 4;
     const uint32_t m = opaque(((j < K) & (c < C)) ? ~0u : 0u);
     xl[j][c * 16 + ((g & 15) ^ (c & 15))] = u32x4{xr[u].x & m, xr[u].y & m, xr[u].z & m, xr[u].w & m};
   }
@@ -788,7 +794,9 @@ __global__ __launch_bounds__(256) void k_moe_down(RowsArgs a, const float *gw, i
   __builtin_amdgcn_sched_barrier(0);
   if (wid < K) finish(wid, DA, okA, EA);
   __builtin_amdgcn_sched_barrier(0);
-  if (wid + 4 < K) finish(wid + 4, DB, okB, EB);
+  if constexpr (WPB == 4) {
+    if (wid + 4 < K) finish(wid + 4, DB, okB, EB);
+  }
   __syncthreads();
   if (tid < TR && row0 + tid < a.rows) {
     float out = 0.f;
@@ -1226,10 +1234,16 @@ hipError_t launch_softcap(float *v, int64_t n, float cap, hipStream_t s) {
 template <class F, int LPR>
 static hipError_t launch_moe_down_cfg(const RowsArgs &a, const float *gw, int32_t T, int32_t K, const DevInfo &dev,
                                       hipStream_t s) {
-  constexpr int TR = F::RT * (64 / LPR);
-  const int64_t n_tiles = (a.rows + TR - 1) / TR;
-  if (n_tiles * T > 2 * (int64_t)dev.cu_count) return hipErrorNotSupported;
-  hipLaunchKernelGGL((k_moe_down<F, LPR>), dim3((unsigned)n_tiles, T), dim3(256), 0, s, a, gw, K);
+  // 8-wave workgroups (twice the rows, half the x staging per row) while one
+  // per CU covers the rows; else 4-wave ones, up to two per CU
+  constexpr int TR8 = 2 * F::RT * (64 / LPR), TR4 = F::RT * (64 / LPR);
+  const int64_t n8 = (a.rows + TR8 - 1) / TR8, n4 = (a.rows + TR4 - 1) / TR4;
+  if (n8 * T <= (int64_t)dev.cu_count) {
+    hipLaunchKernelGGL((k_moe_down<F, LPR, 8>), dim3((unsigned)n8, T), dim3(512), 0, s, a, gw, K);
+    return hipGetLastError();
+  }
+  if (n4 * T > 2 * (int64_t)dev.cu_count) return hipErrorNotSupported;
+  hipLaunchKernelGGL((k_moe_down<F, LPR, 4>), dim3((unsigned)n4, T), dim3(256), 0, s, a, gw, K);
   return hipGetLastError();
 }
 
