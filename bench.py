@@ -310,7 +310,7 @@ class MoeQ4_K(Workload):
         self.name = "moe_q4_k_128x(2816x2048+2048x1408)_top8_t%d" % tokens
         # one token: the down projection and the weighted sum share a launch
         self.dominant_name = ("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE> (routing + gate_up) + " +
-                              ("k_moe_down<FmtQ4_K, 32> (down + weighted sum)" if tokens * 8 * 2 <= 256 else
+                              ("k_moe_down<FmtQ4_K, 32, 8> (down + weighted sum)" if tokens == 1 else
                                "k_rows<FmtQ4_K, 8, 3, XL> (down) + k_moe_combine"))
         base = synth.moe_q4_k(tokens)
         E, D, FF, K = base["n_experts"], base["dim"], base["ff"], base["k"]
