@@ -59,7 +59,7 @@ TRAFFIC_BYTES = {
     "q4_k_batched_8192x2048_m8": 10338048,
     "q4_k_batched_8192x2048_m32": 12697344,
     "q4_k_batched_8192x2048_m64": 15843072,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40341696,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40024256,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 547372448,
     "q5_k_matvec_8192x2048": 11771776,
     "q6_k_matvec_8192x2048": 14137088,
