@@ -73,22 +73,56 @@ G4_DEV bf16x8 nibbles_bf16(uint32_t v0, uint32_t v1) {
   return r;
 }
 
-// TT token tiles and GPW column groups per wave: a workgroup of WPB waves
-// covers WPB * GPW groups (its column split, blockIdx.y) for TT token tiles
-// (token group blockIdx.z) over a range of 16-row tiles (blockIdx.x).  A wave
-// unpacks each weight once for its TT token tiles.
+// sc and m of sub-blocks 2(g & 3) and 2(g & 3) + 1 of a super-block head, in
+// bytes 0 and 1 (getScaleMinK4, Q4_KFloatTensor.kt:70-84)
+G4_DEV void scale_min_pair(const u32x4 &H, int g, uint32_t &scp, uint32_t &mp) {
+  const uint32_t sh = (uint32_t)(g & 1) * 16u;
+  const uint32_t y = H.y >> sh, z = H.z >> sh, w = H.w >> sh;
+  scp = g < 2 ? (y & 0x3F3Fu) : ((w & 0x0F0Fu) | ((y >> 2) & 0x3030u));
+  mp = g < 2 ? (z & 0x3F3Fu) : (((w >> 4) & 0x0F0Fu) | ((z >> 2) & 0x3030u));
+}
+
+// sc and m of sub-blocks 4 hq .. 4 hq + 3 (hq = 0, 1), in bytes 0..3
+G4_DEV void scale_min_quad(const u32x4 &H, int hq, uint32_t &scq, uint32_t &mq) {
+  if (hq == 0) {
+    scq = H.y & 0x3F3F3F3Fu;
+    mq = H.z & 0x3F3F3F3Fu;
+  } else {
+    scq = (H.w & 0x0F0F0F0Fu) | ((H.y >> 2) & 0x30303030u);
+    mq = ((H.w >> 4) & 0x0F0F0F0Fu) | ((H.z >> 2) & 0x30303030u);
+  }
+}
+
+// Two 64-column groups per wave: four 32-weight sub-blocks, the K of one
+// v_mfma_f32_16x16x4_f32, which adds each sub-block's (8 d*sc - dmin*m) sum(x)
+// term for the 16 tokens and 16 rows of a tile in one instruction.
+constexpr int TOK_GPW = 2;
+
+// TT token tiles per wave: a workgroup of WPB waves covers WPB * TOK_GPW groups
+// (its column split, blockIdx.y) for TT token tiles (token group blockIdx.z)
+// over a range of 16-row tiles (blockIdx.x).  A wave unpacks each weight once
+// for its TT token tiles.
+// Per tile, lane (j, n) = (lane / 16, lane % 16) computes the scale of all four
+// of the wave's sub-blocks for its row n (the products it owns are row n's) but
+// the sum(x) coefficient only for sub-block j (the fp32 MFMA's B operand is
+// coefficient[sub-block j][row n]); its A operand, the sum of x over sub-block
+// j for token n, comes once per wave from the matrix cores as a masked sum of
+// the bf16 parts.
 // AL: base and row_stride are multiples of 256 (whole super-blocks per row, the
-// usual case): a lane's weight address then moves by a fixed stride per row
-// tile and each wave's group within the super-block is the same for all rows.
-template <int TT, int GPW, int WPB, bool AL>
+// usual case) and the groups come in pairs: a lane's weight address then moves
+// by a fixed stride per row tile, and the wave's two groups lie in one
+// super-block, whose head is loaded once and whose four sub-blocks' scales
+// take wave-uniform byte positions.
+template <int TT, int WPB, bool AL>
 __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
+  constexpr int GPW = TOK_GPW, NH = AL ? 1 : GPW;
   static_assert(TT * GPW <= TOK_SLOTS && WPB >= TT && WPB % TT == 0, "tile shape");
   __shared__ f32x4 red[2][TT][WPB][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, j = lane >> 4;
   const int C = a.dim1 >> 6;
-  const int g0 = ((int)blockIdx.y * WPB + wid) * GPW;  // first group of this wave's slice
+  const int g0 = ((int)blockIdx.y * WPB + wid) * GPW;  // first group of this wave's slice (even)
   const int ng = max(0, min(GPW, C - g0));                   // wave-uniform
   const int tt0 = (int)blockIdx.z * TT;                      // first token tile
   const int n_rt = (a.rows + 15) >> 4;
@@ -105,19 +139,17 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   const int64_t rs_sb = a.row_stride >> 8;
   const uint8_t *w_row0 = a.W + ((a.base >> 8) + (int64_t)(rt0 * 16 + n) * rs_sb) * 144;
   const int64_t w_step = 16 * rs_sb * 144;
-  auto load_w = [&](int rt, bool live, u32x2a4 (&Q)[GPW], u32x4 (&H)[GPW], int (&gs)[GPW]) {
+  auto load_w = [&](int rt, bool live, u32x2a4 (&Q)[GPW], u32x4 (&H)[NH], int (&gs)[GPW]) {
     const int r = rt * 16 + n;
     const bool rok = live && r < a.rows;
     if constexpr (AL) {
-      const uint8_t *row = w_row0 + (int64_t)(rt - rt0) * w_step;
+      // rows past the end read the tensor's first super-block
+      const uint8_t *sb = rok && ng > 0 ? w_row0 + (int64_t)(rt - rt0) * w_step + (g0 >> 2) * 144 : a.W;
+      H[0] = *(const u32x4 *)sb;
 #pragma unroll
       for (int gi = 0; gi < GPW; ++gi) {
-        const int g = g0 + gi;
-        // rows past the end and groups past the slice read the first super-block
-        const uint8_t *sb = (rok && gi < ng) ? row + (g >> 2) * 144 : a.W;
-        gs[gi] = g & 3;  // wave-uniform
-        H[gi] = *(const u32x4 *)sb;
-        Q[gi] = *(const u32x2a4 *)(sb + 16 + 32 * (g & 3) + 8 * j);
+        gs[gi] = (g0 + gi) & 3;  // wave-uniform
+        Q[gi] = *(const u32x2a4 *)(sb + 16 + 32 * ((g0 + gi) & 3) + 8 * j);
       }
       return;
     }
@@ -154,7 +186,7 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   }
 
   u32x2a4 QA[GPW], QB[GPW];
-  u32x4 HA[GPW], HB[GPW];
+  u32x4 HA[NH], HB[NH];
   int GA[GPW], GB[GPW];
   // the first tile's weight loads go out behind the x loads and before any
   // use of x (vmcnt retires in order: the split below waits for x only)
@@ -162,16 +194,22 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   load_w(rt0, rt0 < rt1, QA, HA, GA);
   __builtin_amdgcn_sched_barrier(0);
 
-  // bf16 parts (A operands) and per-sub-block sums of x, the latter on the
-  // matrix cores as parts x ones: the result lands in the C layout (token
-  // 4 j + i of the tile, any column), fp32-accumulated like the products
+  // bf16 parts (A operands), and per token tile the sum of x over sub-block j
+  // (group j / 2, half j % 2) for token n: the matrix cores add mask_s x parts
+  // over the sub-blocks s, where mask_s is ones on rows 4s .. 4s + 3, so row
+  // 4j + i of the result (this lane's outputs) is sub-block j's sum; the parts
+  // are the B operand here (their register layout is the same), and the sums
+  // are fp32-accumulated like the products
   bf16x8 A[TT][GPW][2][3];
-  float xs[TT][GPW][2][4];
-  bf16x8 ones;
+  float xsT[TT];
+  bf16x8 msk[2 * GPW];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
+  for (int s = 0; s < 2 * GPW; ++s)
 #pragma unroll
-  for (int ti = 0; ti < TT; ++ti)
+    for (int e = 0; e < 8; ++e) msk[s][e] = (__bf16)((n >> 2) == s ? 1.0f : 0.0f);
+#pragma unroll
+  for (int ti = 0; ti < TT; ++ti) {
+    f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi)
 #pragma unroll
@@ -186,57 +224,79 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
           v[4 * u + 3] = __uint_as_float(xr[ti][gi][h][u].w & m);
         }
         split3(v, A[ti][gi][h][0], A[ti][gi][h][1], A[ti][gi][h][2]);
-        f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int p = 0; p < 3; ++p) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[ti][gi][h][p], ones, s, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) xs[ti][gi][h][i] = s[i];
+        for (int p = 0; p < 3; ++p)
+          s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(msk[2 * gi + h], A[ti][gi][h][p], s4, 0, 0, 0);
       }
+    xsT[ti] = s4[0];
+  }
 
-  auto tile = [&](int rt, const u32x2a4 (&Q)[GPW], const u32x4 (&H)[GPW], const int (&gs)[GPW]) {
+  auto tile = [&](int rt, const u32x2a4 (&Q)[GPW], const u32x4 (&H)[NH], const int (&gs)[GPW]) {
     f32x4 acc[TT];
 #pragma unroll
     for (int ti = 0; ti < TT; ++ti) acc[ti] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (ng > 0) {  // wave-uniform
+      // d*sc/16 of the four sub-blocks s (group s / 2, half s % 2) of row n, and
+      // 8 d*sc - dmin*m of sub-block j; d*sc is exact (11 x 6 bits), so is
+      // 8 d*sc = 128 (d*sc/16)
+      float d1[2 * GPW], cj;
+      if constexpr (AL) {
+        const float dq = h2f(H[0].x & 0xFFFFu) * 0.0625f, dmin = h2f(H[0].x >> 16);
+        uint32_t scq, mq;
+        scale_min_quad(H[0], (g0 & 3) >> 1, scq, mq);
 #pragma unroll
-    for (int gi = 0; gi < GPW; ++gi) {
-      if (gi < ng) {  // wave-uniform
-        const uint32_t w0 = Q[gi].x, w1 = Q[gi].y;
-        const bf16x8 bl = nibbles_bf16(opaque(lo_nibbles_s16(w0)), opaque(lo_nibbles_s16(w1)));
-        const bf16x8 bh = nibbles_bf16(opaque(hi_nibbles_s16(w0)), opaque(hi_nibbles_s16(w1)));
-        // getScaleMinK4 (Q4_KFloatTensor.kt:70-84) for sub-blocks 2g, 2g+1 of
-        // this lane's row: bytes 2(g&1), 2(g&1)+1 of the three scale dwords
-        const int g = gs[gi];
-        const uint32_t sh = (uint32_t)(g & 1) * 16u;
-        const uint32_t y = H[gi].y >> sh, z = H[gi].z >> sh, w = H[gi].w >> sh;
-        const uint32_t scp = g < 2 ? (y & 0x3F3Fu) : ((w & 0x0F0Fu) | ((y >> 2) & 0x3030u));
-        const uint32_t mp = g < 2 ? (z & 0x3F3Fu) : (((w >> 4) & 0x0F0Fu) | ((z >> 2) & 0x3030u));
-        const float d = h2f(H[gi].x & 0xFFFFu), dmin = h2f(H[gi].x >> 16);
-        const float ds1 = d * ubyte(scp, 0), ds2 = d * ubyte(scp, 1);  // exact (11 x 6 bits)
-        const float d1 = ds1 * 0.0625f, d2 = ds2 * 0.0625f;
-        const float c1 = __builtin_fmaf(8.f, ds1, -(dmin * ubyte(mp, 0)));
-        const float c2 = __builtin_fmaf(8.f, ds2, -(dmin * ubyte(mp, 1)));
-        // every token tile's products first, then the scale epilogues: the
-        // matrix core works through the independent chains while they drain
-        f32x4 pl[TT], ph[TT];
+        for (int s = 0; s < 4; ++s) d1[s] = dq * ubyte(scq, s);
+        const float scj = (float)((scq >> (8 * j)) & 0xFFu), mj = (float)((mq >> (8 * j)) & 0xFFu);
+        cj = __builtin_fmaf(128.f, dq * scj, -(dmin * mj));
+      } else {
+        float cc[GPW][2];
 #pragma unroll
-        for (int ti = 0; ti < TT; ++ti) pl[ti] = ph[ti] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int gi = 0; gi < GPW; ++gi) {
+          uint32_t scp, mp;
+          scale_min_pair(H[gi], gs[gi], scp, mp);
+          const float dq = h2f(H[gi].x & 0xFFFFu) * 0.0625f, dmin = h2f(H[gi].x >> 16);
 #pragma unroll
-        for (int p = 0; p < 3; ++p)
-#pragma unroll
-          for (int ti = 0; ti < TT; ++ti) {
-            pl[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[ti][gi][0][p], bl, pl[ti], 0, 0, 0);
-            ph[ti] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[ti][gi][1][p], bh, ph[ti], 0, 0, 0);
+          for (int h = 0; h < 2; ++h) {
+            d1[2 * gi + h] = dq * ubyte(scp, h);
+            cc[gi][h] = __builtin_fmaf(128.f, d1[2 * gi + h], -(dmin * ubyte(mp, h)));
           }
-#pragma unroll
-        for (int ti = 0; ti < TT; ++ti)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            acc[ti][i] = __builtin_fmaf(d1, pl[ti][i], acc[ti][i]);
-            acc[ti][i] = __builtin_fmaf(d2, ph[ti][i], acc[ti][i]);
-            acc[ti][i] = __builtin_fmaf(c1, xs[ti][gi][0][i], acc[ti][i]);
-            acc[ti][i] = __builtin_fmaf(c2, xs[ti][gi][1][i], acc[ti][i]);
-          }
+        }
+        const float c0 = (j & 1) ? cc[0][1] : cc[0][0], c1 = (j & 1) ? cc[1][1] : cc[1][0];
+        // a group past the slice has the tensor's first head: no coefficient
+        cj = (j >> 1) >= ng ? 0.f : ((j >> 1) ? c1 : c0);
       }
+      // every product first, then the fp32 MFMA of the sum(x) terms, then the
+      // scales: the matrix core works through the independent chains
+      f32x4 P[TT][GPW][2];
+#pragma unroll
+      for (int gi = 0; gi < GPW; ++gi) {
+        if (gi < ng) {  // wave-uniform
+          const uint32_t w0 = Q[gi].x, w1 = Q[gi].y;
+          const bf16x8 bl = nibbles_bf16(opaque(lo_nibbles_s16(w0)), opaque(lo_nibbles_s16(w1)));
+          const bf16x8 bh = nibbles_bf16(opaque(hi_nibbles_s16(w0)), opaque(hi_nibbles_s16(w1)));
+#pragma unroll
+          for (int ti = 0; ti < TT; ++ti) P[ti][gi][0] = P[ti][gi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int ti = 0; ti < TT; ++ti) {
+              P[ti][gi][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[ti][gi][0][p], bl, P[ti][gi][0], 0, 0, 0);
+              P[ti][gi][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[ti][gi][1][p], bh, P[ti][gi][1], 0, 0, 0);
+            }
+        }
+      }
+#pragma unroll
+      for (int ti = 0; ti < TT; ++ti) acc[ti] = __builtin_amdgcn_mfma_f32_16x16x4f32(xsT[ti], cj, acc[ti], 0, 0, 0);
+#pragma unroll
+      for (int gi = 0; gi < GPW; ++gi)
+        if (gi < ng)
+#pragma unroll
+          for (int ti = 0; ti < TT; ++ti)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              acc[ti][i] = __builtin_fmaf(d1[2 * gi], P[ti][gi][0][i], acc[ti][i]);
+              acc[ti][i] = __builtin_fmaf(d1[2 * gi + 1], P[ti][gi][1][i], acc[ti][i]);
+            }
     }
     // the WPB column slices are summed in wave order (deterministic), the work
     // spread over the waves: wave w takes token tile w / (WPB / TT)'s components
@@ -302,7 +362,7 @@ __global__ __launch_bounds__(256) void k_tok_reduce(const float *part, int split
 // groups and 4/8/16 waves for M = 8..64 at 8192 x 2048, this shape was the
 // fastest or within 2% at every M, and it needs no column split up to 2048
 // columns.
-constexpr int TOK_TT = 1, TOK_GPW = 2, TOK_WPB = 16;
+constexpr int TOK_TT = 1, TOK_WPB = 16;
 
 struct TokShape {
   int splits, tgroups, gx;
@@ -341,10 +401,12 @@ hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_
   const TokShape sh = tok_shape(a, dev);
   if (sh.splits > 1 && !a.part) return hipErrorInvalidValue;
   const dim3 grid((unsigned)sh.gx, (unsigned)sh.splits, (unsigned)sh.tgroups);
-  if ((a.base % 256) == 0 && (a.row_stride % 256) == 0)
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_GPW, TOK_WPB, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
+  // whole super-blocks per row and an even number of groups: every wave's two
+  // groups lie in one super-block
+  if ((a.base % 256) == 0 && (a.row_stride % 256) == 0 && (a.dim1 % 128) == 0)
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
   else
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_GPW, TOK_WPB, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
   if (sh.splits == 1) return hipGetLastError();
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
