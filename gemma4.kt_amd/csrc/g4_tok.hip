@@ -34,6 +34,8 @@
 #include "g4_device.hpp"
 #include "g4_internal.hpp"
 
+#include <type_traits>
+
 namespace g4 {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -42,20 +44,34 @@ typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
 
 constexpr int TOK_SLOTS = 4;  // (token tile, 64-column group) pairs a wave can keep split in registers
 
-// x = p1 + p2 + p3 exactly (each residual is exact in fp32; the third has at
-// most 8 significant bits).  Infinite or NaN x stay in p1 with zero residuals.
+// x = p1 + p2 + p3 exactly: p1 and p2 are the bf16 truncations of x and of
+// x - p1 (their top 8 significant bits), x - p1 - p2 has at most 8 significant
+// bits, and both differences are exact in fp32.  Truncation keeps every part of
+// a finite x finite.  GUARD: an infinite x stays in p1 with zero residuals;
+// without it x - p1 is NaN there, which the caller detects.  A NaN x gives NaN
+// parts either way.
+template <bool GUARD>
 G4_DEV void split3(const float (&v)[8], bf16x8 &p1, bf16x8 &p2, bf16x8 &p3) {
+  uint32_t t1[8], t2[8], t3[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const __bf16 b1 = (__bf16)v[e];
-    const float f1 = (float)b1;
-    const float r1 = __builtin_isfinite(f1) ? v[e] - f1 : 0.f;
-    const __bf16 b2 = (__bf16)r1;
-    const float r2 = r1 - (float)b2;
-    p1[e] = b1;
-    p2[e] = b2;
-    p3[e] = (__bf16)r2;
+    t1[e] = __float_as_uint(v[e]) & 0xFFFF0000u;
+    float r1 = v[e] - __uint_as_float(t1[e]);
+    if (GUARD) r1 = __builtin_isinf(v[e]) ? 0.f : r1;
+    t2[e] = __float_as_uint(r1) & 0xFFFF0000u;
+    t3[e] = __float_as_uint(r1 - __uint_as_float(t2[e]));
   }
+  // two values' upper halves per dword (v_perm_b32)
+  u32x4 a, b, c;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    a[k] = __builtin_amdgcn_perm(t1[2 * k + 1], t1[2 * k], 0x07060302u);
+    b[k] = __builtin_amdgcn_perm(t2[2 * k + 1], t2[2 * k], 0x07060302u);
+    c[k] = __builtin_amdgcn_perm(t3[2 * k + 1], t3[2 * k], 0x07060302u);
+  }
+  p1 = __builtin_bit_cast(bf16x8, a);
+  p2 = __builtin_bit_cast(bf16x8, b);
+  p3 = __builtin_bit_cast(bf16x8, c);
 }
 
 // bf16 of 16(q - 8) for the 8 nibbles of one K-slice.  A nibble q moved to the
@@ -106,8 +122,7 @@ constexpr int TOK_GPW = 2;
 // of the wave's sub-blocks for its row n (the products it owns are row n's) but
 // the sum(x) coefficient only for sub-block j (the fp32 MFMA's B operand is
 // coefficient[sub-block j][row n]); its A operand, the sum of x over sub-block
-// j for token n, comes once per wave from the matrix cores as a masked sum of
-// the bf16 parts.
+// j for token n, is formed once per wave.
 // AL: base and row_stride are multiples of 256 (whole super-blocks per row, the
 // usual case) and the groups come in pairs: a lane's weight address then moves
 // by a fixed stride per row tile, and the wave's two groups lie in one
@@ -117,7 +132,13 @@ template <int TT, int WPB, bool AL>
 __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   constexpr int GPW = TOK_GPW, NH = AL ? 1 : GPW;
   static_assert(TT * GPW <= TOK_SLOTS && WPB >= TT && WPB % TT == 0, "tile shape");
-  __shared__ f32x4 red[2][TT][WPB][64];
+  // LDS: first each wave's x slice (16 tokens x 128 columns, rows padded to
+  // XROW floats so the reads below are conflict-free), then, after a barrier,
+  // the cross-wave partial tiles
+  constexpr int XROW = 132;
+  constexpr size_t RED_BYTES = sizeof(f32x4) * 2 * TT * WPB * 64, XST_BYTES = sizeof(float) * WPB * 16 * XROW;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[RED_BYTES > XST_BYTES ? RED_BYTES : XST_BYTES];
+  f32x4(*red)[TT][WPB][64] = (f32x4(*)[TT][WPB][64])lds;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, j = lane >> 4;
@@ -166,25 +187,19 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
     }
   };
 
-  // x slice: token (tt0 + ti) * 16 + n, columns 64 g + 32 h + 8 j .. +8
-  u32x4a4 xr[TT][GPW][2][2];
-  bool tok_ok[TT];
+  // x slice: 16 tokens x the wave's 128 columns, read so that adjacent lanes
+  // take adjacent 16-byte pieces (each instruction two tokens' 512 contiguous
+  // bytes: lane l takes piece l % 32 of token 2q + l / 32) and staged in LDS;
+  // columns of groups past the slice come from group 0 (in bounds, never used)
+  u32x4a4 xg[TT][8];
 #pragma unroll
-  for (int ti = 0; ti < TT; ++ti) {
-    const int tok = (tt0 + ti) * 16 + n;
-    tok_ok[ti] = tok < a.M;
-    const float *xt = a.x + (int64_t)(tok_ok[ti] ? tok : 0) * a.x_stride;
+  for (int ti = 0; ti < TT; ++ti)
 #pragma unroll
-    for (int gi = 0; gi < GPW; ++gi)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int g = gi < ng ? g0 + gi : 0;
-        const u32x4a4 *p = (const u32x4a4 *)(xt + (int64_t)g * 64 + 32 * h + 8 * j);
-        xr[ti][gi][h][0] = p[0];
-        xr[ti][gi][h][1] = p[1];
-      }
-  }
-
+    for (int q = 0; q < 8; ++q) {
+      const int tok = (tt0 + ti) * 16 + 2 * q + (lane >> 5), c = lane & 31, gi = c >> 4;
+      const float *p = a.x + (int64_t)(tok < a.M ? tok : 0) * a.x_stride + (int64_t)(gi < ng ? g0 + gi : 0) * 64 + 4 * (c & 15);
+      xg[ti][q] = *(const u32x4a4 *)p;
+    }
   u32x2a4 QA[GPW], QB[GPW];
   u32x4 HA[NH], HB[NH];
   int GA[GPW], GB[GPW];
@@ -194,42 +209,83 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   load_w(rt0, rt0 < rt1, QA, HA, GA);
   __builtin_amdgcn_sched_barrier(0);
 
-  // bf16 parts (A operands), and per token tile the sum of x over sub-block j
-  // (group j / 2, half j % 2) for token n: the matrix cores add mask_s x parts
-  // over the sub-blocks s, where mask_s is ones on rows 4s .. 4s + 3, so row
-  // 4j + i of the result (this lane's outputs) is sub-block j's sum; the parts
-  // are the B operand here (their register layout is the same), and the sums
-  // are fp32-accumulated like the products
-  bf16x8 A[TT][GPW][2][3];
-  float xsT[TT];
-  bf16x8 msk[2 * GPW];
-#pragma unroll
-  for (int s = 0; s < 2 * GPW; ++s)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) msk[s][e] = (__bf16)((n >> 2) == s ? 1.0f : 0.0f);
+  // back from LDS in the MFMA layout: lane (j, n) takes token n, columns
+  // 64 gi + 32 h + 8 j .. +8 of the slice (the K-slice j of sub-block (gi, h));
+  // a wave reads only what it wrote, and LDS operations of a wave run in order
+  u32x4a4 xr[TT][GPW][2][2];
+  float *xst = (float *)lds + wid * 16 * XROW;
 #pragma unroll
   for (int ti = 0; ti < TT; ++ti) {
-    f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 8; ++q) *(u32x4 *)(xst + (2 * q + (lane >> 5)) * XROW + 4 * (lane & 31)) = xg[ti][q];
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) xr[ti][gi][h][u] = *(const u32x4 *)(xst + n * XROW + 64 * gi + 32 * h + 8 * j + 4 * u);
+  }
+  __syncthreads();  // every wave has its x: the LDS now holds the partial tiles
+
+  // Per token tile, the sum of x over sub-block j (group j / 2, half j % 2) for
+  // token n, the fp32 MFMA's A operand: each lane adds its 8 values of each
+  // sub-block, and a transposing butterfly over the four K-slice lanes of the
+  // token leaves sub-block j's sum in row j.  x is not masked: the tokens past M
+  // (token 0's x) only reach their own output rows, which are never stored, and
+  // groups past the slice are never multiplied and get no coefficient.
+  float xsT[TT];
+  bool bad = false;
+#pragma unroll
+  for (int ti = 0; ti < TT; ++ti) {
+    float ps[2 * GPW];
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const uint32_t m = opaque((tok_ok[ti] && gi < ng) ? ~0u : 0u);
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          v[4 * u] = __uint_as_float(xr[ti][gi][h][u].x & m);
-          v[4 * u + 1] = __uint_as_float(xr[ti][gi][h][u].y & m);
-          v[4 * u + 2] = __uint_as_float(xr[ti][gi][h][u].z & m);
-          v[4 * u + 3] = __uint_as_float(xr[ti][gi][h][u].w & m);
-        }
-        split3(v, A[ti][gi][h][0], A[ti][gi][h][1], A[ti][gi][h][2]);
-#pragma unroll
-        for (int p = 0; p < 3; ++p)
-          s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(msk[2 * gi + h], A[ti][gi][h][p], s4, 0, 0, 0);
+        float t = __uint_as_float(xr[ti][gi][h][0].x);
+        t += __uint_as_float(xr[ti][gi][h][0].y);
+        t += __uint_as_float(xr[ti][gi][h][0].z);
+        t += __uint_as_float(xr[ti][gi][h][0].w);
+        t += __uint_as_float(xr[ti][gi][h][1].x);
+        t += __uint_as_float(xr[ti][gi][h][1].y);
+        t += __uint_as_float(xr[ti][gi][h][1].z);
+        t += __uint_as_float(xr[ti][gi][h][1].w);
+        ps[2 * gi + h] = t;
       }
-    xsT[ti] = s4[0];
+    static_assert(GPW == 2, "four sub-blocks per wave");
+    const float t02 = tstep<32>(ps[0], ps[2], lane), t13 = tstep<32>(ps[1], ps[3], lane);
+    xsT[ti] = tstep<16>(t02, t13, lane);
+    bad |= !__builtin_isfinite(xsT[ti]);
   }
+  // bf16 parts (A operands).  The split without the infinity guard runs unless
+  // some sum in the wave is infinite or NaN (an activation is, or a sum
+  // overflowed): wave-uniform
+  bf16x8 A[TT][GPW][2][3];
+  auto split_all = [&](auto guard) {
+#pragma unroll
+    for (int ti = 0; ti < TT; ++ti)
+#pragma unroll
+      for (int gi = 0; gi < GPW; ++gi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float v[8];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            v[4 * u] = __uint_as_float(xr[ti][gi][h][u].x);
+            v[4 * u + 1] = __uint_as_float(xr[ti][gi][h][u].y);
+            v[4 * u + 2] = __uint_as_float(xr[ti][gi][h][u].z);
+            v[4 * u + 3] = __uint_as_float(xr[ti][gi][h][u].w);
+          }
+          split3<decltype(guard)::value>(v, A[ti][gi][h][0], A[ti][gi][h][1], A[ti][gi][h][2]);
+        }
+  };
+  if (__builtin_amdgcn_ballot_w64(bad) != 0)
+    split_all(std::true_type());
+  else
+    split_all(std::false_type());
+#pragma unroll
+  for (int ti = 0; ti < TT; ++ti)
+    if ((j >> 1) >= ng) xsT[ti] = 0.f;  // a group past the slice
 
   auto tile = [&](int rt, const u32x2a4 (&Q)[GPW], const u32x4 (&H)[NH], const int (&gs)[GPW]) {
     f32x4 acc[TT];

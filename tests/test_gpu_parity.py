@@ -417,6 +417,30 @@ def test_q4_k_batched_matrix_core_shapes(g4, ctx, oracle, m, rows, dim1, off_row
         assert_dots(Y[i], ex, ab, "token %d" % i)
 
 
+@pytest.mark.parametrize("rows,dim1", [(40, 2048), (34, 1408)])
+def test_q4_k_batched_matrix_core_non_finite_x(g4, ctx, oracle, rows, dim1):
+    """+inf, NaN and -inf activations in three of five tokens: those tokens' outputs are
+    all non-finite, as the reference's are (inf * w and NaN * w reach every row), and
+    the finite tokens, which share the kernel's waves with them, stay within the bound.
+    Rows of whole super-blocks (2048) and rows that start mid super-block (1408)."""
+    announce("q4_k batched non-finite x rows=%d dim1=%d" % (rows, dim1))
+    m = 5
+    raw = synth.weights(54, "mcnf%d" % dim1, Q4_K, rows * dim1)
+    X = synth.activations(54, "mcnfx%d" % dim1, m * dim1).reshape(m, dim1)
+    X[1, 5] = np.inf
+    X[2, dim1 // 3] = np.nan
+    X[3, dim1 - 7] = -np.inf
+    w = upload(g4, ctx, Q4_K, raw, rows * dim1)
+    Y = w.matmul_batch(X, rows, dim1)
+    for i in range(m):
+        ex, ab = oracle.matmul_exact(Q4_K, raw, X[i], rows, dim1)
+        if i in (1, 2, 3):
+            assert not np.any(np.isfinite(ex))
+            assert not np.any(np.isfinite(Y[i])), "token %d: finite outputs %r" % (i, Y[i][np.isfinite(Y[i])][:4])
+        else:
+            assert_dots(Y[i], ex, ab, "token %d" % i)
+
+
 def test_q4_k_batched_matrix_core_wide_range_x(g4, ctx, oracle):
     """x spanning 1e-20..1e20: the three bf16 parts of x are exact at every magnitude."""
     announce("q4_k batched wide-range x")
