@@ -135,9 +135,12 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   // LDS: first each wave's x slice (16 tokens x 128 columns, rows padded to
   // XROW floats so the reads below are conflict-free), then, after a barrier,
   // the cross-wave partial tiles
-  constexpr int XROW = 132;
+  // (and with AL each wave's staged weight tile, 16 rows x 80 bytes)
+  constexpr int XROW = 132, WROW = 80;
   constexpr size_t RED_BYTES = sizeof(f32x4) * 2 * TT * WPB * 64, XST_BYTES = sizeof(float) * WPB * 16 * XROW;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[RED_BYTES > XST_BYTES ? RED_BYTES : XST_BYTES];
+  constexpr size_t WST_BYTES = AL ? (size_t)WPB * 16 * WROW : 0;
+  __shared__ __attribute__((aligned(16))) unsigned char
+      lds[RED_BYTES + WST_BYTES > XST_BYTES ? RED_BYTES + WST_BYTES : XST_BYTES];
   f32x4(*red)[TT][WPB][64] = (f32x4(*)[TT][WPB][64])lds;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -187,6 +190,31 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
     }
   };
 
+  // AL: a tile's weights for this wave, 16 rows x (head + the wave's two
+  // groups), read by four adjacent lanes per row (row lane / 4: bytes
+  // 16 (lane % 4) of the 64 group bytes and dword lane % 4 of the head, where
+  // loading them by row n = lane % 16 would put 16 rows 1152 bytes apart in
+  // every instruction) and staged in the wave's own LDS rows, from where each
+  // lane takes its row's head and its K-slice of both groups
+  unsigned char *wst = lds + RED_BYTES + (size_t)wid * 16 * WROW;
+  const uint8_t *w_tile0 = a.W + ((a.base >> 8) + (int64_t)(rt0 * 16 + (lane >> 2)) * rs_sb + (g0 >> 2)) * 144;
+  auto load_raw = [&](int rt, bool live, u32x4 &QR, uint32_t &HR) {
+    // rows past the end read the tensor's first super-block
+    const bool ok = live && ng > 0 && rt * 16 + (lane >> 2) < a.rows;
+    const uint8_t *sb = ok ? w_tile0 + (int64_t)(rt - rt0) * w_step : a.W;
+    QR = *(const u32x4 *)(sb + 16 + 32 * (g0 & 3) + 16 * (lane & 3));
+    HR = *(const uint32_t *)(sb + 4 * (lane & 3));
+  };
+  auto stage = [&](const u32x4 &QR, uint32_t HR, u32x2a4 (&Q)[GPW], u32x4 (&H)[NH]) {
+    unsigned char *wr = wst + (lane >> 2) * WROW;
+    *(u32x4 *)(wr + 16 + 16 * (lane & 3)) = QR;
+    *(uint32_t *)(wr + 4 * (lane & 3)) = HR;
+    const unsigned char *rd = wst + n * WROW;
+    H[0] = *(const u32x4 *)rd;
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi) Q[gi] = *(const u32x2a4 *)(rd + 16 + 32 * gi + 8 * j);
+  };
+
   // x slice: 16 tokens x the wave's 128 columns, read so that adjacent lanes
   // take adjacent 16-byte pieces (each instruction two tokens' 512 contiguous
   // bytes: lane l takes piece l % 32 of token 2q + l / 32) and staged in LDS;
@@ -203,10 +231,15 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   u32x2a4 QA[GPW], QB[GPW];
   u32x4 HA[NH], HB[NH];
   int GA[GPW], GB[GPW];
+  u32x4 QRA, QRB;
+  uint32_t HRA, HRB;
   // the first tile's weight loads go out behind the x loads and before any
   // use of x (vmcnt retires in order: the split below waits for x only)
   __builtin_amdgcn_sched_barrier(0);
-  load_w(rt0, rt0 < rt1, QA, HA, GA);
+  if constexpr (AL)
+    load_raw(rt0, rt0 < rt1, QRA, HRA);
+  else
+    load_w(rt0, rt0 < rt1, QA, HA, GA);
   __builtin_amdgcn_sched_barrier(0);
 
   // back from LDS in the MFMA layout: lane (j, n) takes token n, columns
@@ -287,7 +320,8 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   for (int ti = 0; ti < TT; ++ti)
     if ((j >> 1) >= ng) xsT[ti] = 0.f;  // a group past the slice
 
-  auto tile = [&](int rt, const u32x2a4 (&Q)[GPW], const u32x4 (&H)[NH], const int (&gs)[GPW]) {
+  // mid() runs between the partial tile's LDS store and the barrier
+  auto tile = [&](int rt, const u32x2a4 (&Q)[GPW], const u32x4 (&H)[NH], const int (&gs)[GPW], auto &&mid) {
     f32x4 acc[TT];
 #pragma unroll
     for (int ti = 0; ti < TT; ++ti) acc[ti] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -359,6 +393,7 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
     // i = c, c + WPB/TT, ... of every lane's 4 outputs (c = w % (WPB / TT))
 #pragma unroll
     for (int ti = 0; ti < TT; ++ti) red[buf][ti][wid][lane] = acc[ti];
+    mid();
     __syncthreads();
     {
       constexpr int WPT = WPB / TT;  // waves per token tile
@@ -376,16 +411,32 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
     buf ^= 1;
   };
 
-  // two row tiles in flight: tile t+1 loads while tile t multiplies
-  for (int rt = rt0; rt < rt1; rt += 2) {
-    load_w(rt + 1, rt + 1 < rt1, QB, HB, GB);
-    __builtin_amdgcn_sched_barrier(0);
-    tile(rt, QA, HA, GA);
-    __builtin_amdgcn_sched_barrier(0);
-    load_w(rt + 2, rt + 2 < rt1, QA, HA, GA);
-    __builtin_amdgcn_sched_barrier(0);
-    if (rt + 1 < rt1) tile(rt + 1, QB, HB, GB);
-    __builtin_amdgcn_sched_barrier(0);
+  if constexpr (AL) {
+    // tile t+1's weights load while tile t multiplies, and are staged between
+    // tile t's partial store and its barrier
+    stage(QRA, HRA, QA, HA);
+    for (int rt = rt0; rt < rt1; rt += 2) {
+      load_raw(rt + 1, rt + 1 < rt1, QRB, HRB);
+      __builtin_amdgcn_sched_barrier(0);
+      tile(rt, QA, HA, GA, [&] { stage(QRB, HRB, QA, HA); });
+      __builtin_amdgcn_sched_barrier(0);
+      load_raw(rt + 2, rt + 2 < rt1, QRA, HRA);
+      __builtin_amdgcn_sched_barrier(0);
+      if (rt + 1 < rt1) tile(rt + 1, QA, HA, GA, [&] { stage(QRA, HRA, QA, HA); });
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    // two row tiles in flight: tile t+1 loads while tile t multiplies
+    for (int rt = rt0; rt < rt1; rt += 2) {
+      load_w(rt + 1, rt + 1 < rt1, QB, HB, GB);
+      __builtin_amdgcn_sched_barrier(0);
+      tile(rt, QA, HA, GA, [] {});
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(rt + 2, rt + 2 < rt1, QA, HA, GA);
+      __builtin_amdgcn_sched_barrier(0);
+      if (rt + 1 < rt1) tile(rt + 1, QB, HB, GB, [] {});
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 }
 
