@@ -56,23 +56,36 @@ __global__ __launch_bounds__(64 * WPB) void k_wide(RowsArgs a, int rows_per_wg) 
     }
   };
 
-  // x of this lane's chunk, loaded first, then the first tile, and only then
-  // waited for (vmcnt retires in issue order).  Lanes l and l ^ 32 hold the same
-  // chunk (LPR = 32): each loads half of its 16 words and v_permlane32_swap
-  // hands each half the other's, halving x's requests (x's arrival, not the
-  // weights', gates the first tile: the 32 KB vector goes to every workgroup).
+  // x of the wave's 32 chunks, loaded first, then the first tile, and only then
+  // waited for (vmcnt retires in issue order): x's arrival, not the weights',
+  // gates the first tile (the 32 KB vector goes to every workgroup).  Read so
+  // that adjacent lanes take adjacent 16-byte pieces (instruction i: lane l takes
+  // piece l % 16 of chunk 4 i + l / 16; reading by chunk put 64 chunks 256 bytes
+  // apart in every instruction) and staged in the wave's own LDS rows (chunks
+  // padded to XC floats, conflict-free below), a wave reading only what it
+  // wrote.  Lanes l and l ^ 32 hold the same chunk (LPR = 32): each reads half
+  // of its 16 words back and v_permlane32_swap hands each half the other's.
   static_assert(LPR == 32, "two lane groups share each chunk of x");
+  constexpr int XC = 68;
+  __shared__ __attribute__((aligned(16))) float xst[WPB][LPR * XC];
   const int xh = lane >> 5;
-  u32x4a4 xr[8];
-  const u32x4a4 *xp = (const u32x4a4 *)(x + (int64_t)(cok ? c : 0) * 64) + 8 * xh;
+  u32x4a4 xg[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) xr[i] = xp[i];
+  for (int i = 0; i < 8; ++i) {
+    const int cc = wid * LPR + 4 * i + (lane >> 4);  // chunks past the row read chunk 0 (in bounds, masked)
+    xg[i] = *(const u32x4a4 *)(x + (int64_t)(cc < C ? cc : 0) * 64 + 4 * (lane & 15));
+  }
   uint32_t DA[RT][NDW], DB[RT][NDW];
   bool okA[RT], okB[RT];
   int64_t EA[RT], EB[RT];
   __builtin_amdgcn_sched_barrier(0);
   load_tile(0, 0 < n_tiles, DA, okA, EA);
   __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) *(u32x4 *)&xst[wid][(4 * i + (lane >> 4)) * XC + 4 * (lane & 15)] = xg[i];
+  u32x4 xr[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xr[i] = *(const u32x4 *)&xst[wid][q * XC + 32 * xh + 4 * i];
   float xv[64];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
