@@ -51,21 +51,21 @@ Q8_0, Q4_0, Q4_K = 8, 2, 12
 # Recorded in profiles/hbm_traffic_fetch_write_size.md (same command and kernels).
 # "name:part" keys give the other separately timed launches of a step.
 TRAFFIC_BYTES = {
-    "q4_0_ffn_decode_token": 19201792,
-    "q4_0_ffn_decode_token:down": 9816960,
-    "q8_0_matvec_2048x2048": 4638592,
-    "q8_0_lm_head_262144x2048_argmax": 572075040,
+    "q4_0_ffn_decode_token": 19202816,
+    "q4_0_ffn_decode_token:down": 9825152,
+    "q8_0_matvec_2048x2048": 4633472,
+    "q8_0_lm_head_262144x2048_argmax": 572094112,
     "q4_k_batched_8192x2048_m1": 9658240,
-    "q4_k_batched_8192x2048_m8": 10338048,
-    "q4_k_batched_8192x2048_m32": 12697344,
-    "q4_k_batched_8192x2048_m64": 15843072,
+    "q4_k_batched_8192x2048_m8": 10354432,
+    "q4_k_batched_8192x2048_m32": 12713728,
+    "q4_k_batched_8192x2048_m64": 15859456,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40024256,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 547372448,
-    "q5_k_matvec_8192x2048": 11771776,
-    "q6_k_matvec_8192x2048": 14137088,
-    "q4_0_ffn_block_decode_token": 29116672,
-    "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572359552,
-    "attention_decode_h16_kv8_d256_len8192": 136787104,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 546615680,
+    "q5_k_matvec_8192x2048": 11775872,
+    "q6_k_matvec_8192x2048": 14131968,
+    "q4_0_ffn_block_decode_token": 29148800,
+    "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572333824,
+    "attention_decode_h16_kv8_d256_len8192": 136787136,
 }
 
 
@@ -267,7 +267,7 @@ class BatchedQ4_K(Workload):
         # more: the matrix-core kernel (one column split up to 2048 columns, more
         # splits summed by k_tok_reduce)
         self.dominant_name = ("k_rows<FmtQ4_K, 32, EPI_STORE>" if m <= 2 else
-                              "k_tok_q4k<1, 2, 16> (bf16x3 MFMA 16x16x32)")
+                              "k_tok_q4k<1, 16, true> (bf16x3 MFMA 16x16x32)")
         self.name = "q4_k_batched_8192x2048_m%d" % m
         R, D = c["dim0"], c["dim1"]
         self.R, self.D = R, D
