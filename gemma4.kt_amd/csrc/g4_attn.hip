@@ -220,60 +220,82 @@ __global__ __launch_bounds__(256) void k_att_part(AttArgs a) {
 // sum_c w_c l_c and out = sum_c w_c o_c / sum.  Workgroup (head, 64-element
 // slice): wave w takes chunks w, w + 4, ...; the four wave sums are added in wave
 // order.  PRE: up to 128 chunks, every partial is loaded at the start (they do not
-// depend on the maxima), so the kernel makes one round trip to memory.
+// depend on the maxima), so the kernel makes one round trip to memory, and each
+// wave forms M, the weights and the sum itself (no block-wide reduction).
 template <bool PRE>
 __global__ __launch_bounds__(256) void k_att_combine(const float *part, const float *ml, int32_t n_chunks,
                                                      int32_t n_heads, int32_t hs, float *out) {
-  __shared__ float wc[ATT_MAXCHUNKS];
-  __shared__ float red[4];
-  __shared__ float bm;
   __shared__ float ws[4][64];
-  constexpr int NP = PRE ? 32 : 1;
   const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int e = blockIdx.y * 64 + lane;
   const bool live = e < hs;
   const int64_t col = (int64_t)h * hs + (live ? e : 0);
-  float p[NP];
+  float o = 0.f, tot;
   if constexpr (PRE) {
+    // up to 128 chunks: every partial goes out at the start, and every wave
+    // forms the chunk weights itself (lane i: chunks i and i + 64), so the only
+    // barrier is the cross-wave sum at the end
+    constexpr int NP = 32;
+    float p[NP];
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
       const int c = wid + 4 * k;
       p[k] = part[(int64_t)(c < n_chunks ? c : 0) * n_heads * hs + col];
     }
-  }
-  float m = -__builtin_inff(), lc[ATT_MAXCHUNKS / 256];
+    float mc[2], lc[2], w[2];
 #pragma unroll
-  for (int k = 0; k < ATT_MAXCHUNKS / 256; ++k) {
-    const int c = tid + 256 * k;
-    const bool in = c < n_chunks;
-    const float mc = ml[((int64_t)(in ? c : 0) * n_heads + h) * 2];
-    lc[k] = ml[((int64_t)(in ? c : 0) * n_heads + h) * 2 + 1];
-    if (in) wc[c] = mc, m = jmax(m, mc);
-  }
-  m = wave_jmax(m);
-  if (lane == 0) red[wid] = m;
-  __syncthreads();
-  if (tid == 0) bm = jmax(jmax(jmax(red[0], red[1]), red[2]), red[3]);
-  __syncthreads();
-  const float M = bm;
-  float l = 0.f;
-#pragma unroll
-  for (int k = 0; k < ATT_MAXCHUNKS / 256; ++k) {
-    const int c = tid + 256 * k;
-    if (c < n_chunks) {
-      const float w = (float)exp((double)__fsub_rn(wc[c], M));
-      wc[c] = w;
-      l = __builtin_fmaf(w, lc[k], l);
+    for (int q = 0; q < 2; ++q) {
+      const int c = lane + 64 * q;
+      const bool in = c < n_chunks;
+      mc[q] = ml[((int64_t)(in ? c : 0) * n_heads + h) * 2];
+      lc[q] = ml[((int64_t)(in ? c : 0) * n_heads + h) * 2 + 1];
+      if (!in) mc[q] = -__builtin_inff();
     }
-  }
-  __syncthreads();  // red[] reused, every weight stored
-  const float tot = block_sum256(l, red);
-  float o = 0.f;
-  if constexpr (PRE) {
+    const float M = wave_jmax(jmax(mc[0], mc[1]));
+    float l = 0.f;
 #pragma unroll
-    for (int k = 0; k < NP; ++k)
-      if (wid + 4 * k < n_chunks) o = __builtin_fmaf(wc[wid + 4 * k], p[k], o);
+    for (int q = 0; q < 2; ++q) {
+      w[q] = lane + 64 * q < n_chunks ? (float)exp((double)__fsub_rn(mc[q], M)) : 0.f;
+      l = __builtin_fmaf(w[q], lc[q], l);
+    }
+    tot = wave_sum(l);
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      const int c = wid + 4 * k;  // wave-uniform; chunk c's weight sits in lane c % 64 of w[c / 64]
+      const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[k < 16 ? 0 : 1]), c & 63));
+      if (c < n_chunks) o = __builtin_fmaf(wc, p[k], o);
+    }
   } else {
+    __shared__ float wc[ATT_MAXCHUNKS];
+    __shared__ float red[4];
+    __shared__ float bm;
+    float m = -__builtin_inff(), lc[ATT_MAXCHUNKS / 256];
+#pragma unroll
+    for (int k = 0; k < ATT_MAXCHUNKS / 256; ++k) {
+      const int c = tid + 256 * k;
+      const bool in = c < n_chunks;
+      const float mc = ml[((int64_t)(in ? c : 0) * n_heads + h) * 2];
+      lc[k] = ml[((int64_t)(in ? c : 0) * n_heads + h) * 2 + 1];
+      if (in) wc[c] = mc, m = jmax(m, mc);
+    }
+    m = wave_jmax(m);
+    if (lane == 0) red[wid] = m;
+    __syncthreads();
+    if (tid == 0) bm = jmax(jmax(jmax(red[0], red[1]), red[2]), red[3]);
+    __syncthreads();
+    const float M = bm;
+    float l = 0.f;
+#pragma unroll
+    for (int k = 0; k < ATT_MAXCHUNKS / 256; ++k) {
+      const int c = tid + 256 * k;
+      if (c < n_chunks) {
+        const float w = (float)exp((double)__fsub_rn(wc[c], M));
+        wc[c] = w;
+        l = __builtin_fmaf(w, lc[k], l);
+      }
+    }
+    __syncthreads();  // red[] reused, every weight stored
+    tot = block_sum256(l, red);
     constexpr int UC = 8;
     for (int c0 = wid; c0 < n_chunks; c0 += 4 * UC) {
       float q[UC];
