@@ -28,10 +28,26 @@ G4_DEV float jmax(float a, float b) {  // java.lang.Math.max(float, float)
   return a >= b ? a : b;
 }
 
-G4_DEV float wave_jmax(float v) {
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) v = jmax(v, __shfl_xor(v, s, 64));
-  return v;
+// Sum over the wave in every lane, without LDS (permlane swaps at distances 32
+// and 16, DPP below; each step adds a lane's value and its partner's, the same
+// bits in either order, so every lane ends with the same sum).
+G4_DEV float wave_fsum(float v) {
+  v = pstep<32>(v);
+  v = pstep<16>(v);
+  v = pstep<8>(v);
+  v = pstep<4>(v);
+  v = pstep<2>(v);
+  return pstep<1>(v);
+}
+
+G4_DEV float wave_jmax(float v) {  // every lane: the wave's maximum (butterfly without LDS)
+  const int lane = threadIdx.x & 63;
+  v = jmax(v, __uint_as_float(partner_u32<32>(__float_as_uint(v), lane)));
+  v = jmax(v, __uint_as_float(partner_u32<16>(__float_as_uint(v), lane)));
+  v = jmax(v, __uint_as_float(partner_u32<8>(__float_as_uint(v), lane)));
+  v = jmax(v, __uint_as_float(partner_u32<4>(__float_as_uint(v), lane)));
+  v = jmax(v, __uint_as_float(partner_u32<2>(__float_as_uint(v), lane)));
+  return jmax(v, __uint_as_float(partner_u32<1>(__float_as_uint(v), lane)));
 }
 
 template <int HS, int GT>
@@ -148,7 +164,7 @@ __global__ __launch_bounds__(256) void k_att_part(AttArgs a) {
   if (wid < GT) {
     float l = 0.f;
     for (int r = lane; r < nr; r += 64) l += sc[r][wid];
-    l = wave_sum(l);
+    l = wave_fsum(l);
     if (lane == 0) mls[1][wid] = l;
   }
 
@@ -258,7 +274,7 @@ __global__ __launch_bounds__(256) void k_att_combine(const float *part, const fl
       w[q] = lane + 64 * q < n_chunks ? (float)exp((double)__fsub_rn(mc[q], M)) : 0.f;
       l = __builtin_fmaf(w[q], lc[q], l);
     }
-    tot = wave_sum(l);
+    tot = wave_fsum(l);
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
       const int c = wid + 4 * k;  // wave-uniform; chunk c's weight sits in lane c % 64 of w[c / 64]
