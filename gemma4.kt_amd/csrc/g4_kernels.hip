@@ -483,7 +483,13 @@ __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
     const int k = q / (LPR / RT);
     const bool writer = (q % (LPR / RT)) == 0;
     if constexpr (EPI == EPI_GELU_PAIR) {
-      const float up = __shfl_xor(r, LPR / 2, 64);
+      // the up row's value from lane ^ LPR/2: a permlane swap or DPP for 32, 16
+      // and 8 (exact xor partners), an LDS shuffle below
+      float up;
+      if constexpr (LPR / 2 == 32 || LPR / 2 == 16 || LPR / 2 == 8)
+        up = __uint_as_float(partner_u32<LPR / 2>(__float_as_uint(r), lane));
+      else
+        up = __shfl_xor(r, LPR / 2, 64);
       if (writer && k < RT / 2) gq[wid][gq_n + (k % (RT / 2)) * RPW + gi] = make_float2(r, up);
       gq_n += LRT;
       if (gq_n + LRT > 64) gq_flush();
