@@ -136,8 +136,14 @@ G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *
 #pragma unroll
   for (int u = 0; u < PER; ++u)
     if (tid + 256 * u < E) m = java_max(m, lv[u]);
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) m = java_max(m, __shfl_xor(m, s, 64));
+  // over the wave without LDS (permlane swaps, then DPP; the half-row mirror at
+  // distance 4 pairs lanes of the two halves of every 8, which serves a maximum)
+  m = java_max(m, __uint_as_float(partner_u32<32>(__float_as_uint(m), lane)));
+  m = java_max(m, __uint_as_float(partner_u32<16>(__float_as_uint(m), lane)));
+  m = java_max(m, __uint_as_float(partner_u32<8>(__float_as_uint(m), lane)));
+  m = java_max(m, __uint_as_float(partner_u32<4>(__float_as_uint(m), lane)));
+  m = java_max(m, __uint_as_float(partner_u32<2>(__float_as_uint(m), lane)));
+  m = java_max(m, __uint_as_float(partner_u32<1>(__float_as_uint(m), lane)));
   if (lane == 0) r.wm[wid] = m;
   __syncthreads();
   m = java_max(java_max(r.wm[0], r.wm[1]), java_max(r.wm[2], r.wm[3]));
@@ -246,8 +252,16 @@ G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *
       }
       for (; j < j1; ++j) r0 += (int)(r.key[j] > ki);
       int rank = (r0 + r1) + (r2 + r3);
-      // the parts of one element are adjacent lanes of one wave
-      for (int o = 1; o < parts; o <<= 1) rank += __shfl_xor(rank, o, 64);
+      // the parts of one element are adjacent lanes of one wave (parts is a power
+      // of two, wave-uniform): sums over 2, 4, 8, ... lanes, without LDS (at
+      // distance 4 the half-row mirror pairs the two quads of every 8 lanes,
+      // which after the steps at 1 and 2 gives the same sum as lane ^ 4)
+      if (parts > 1) rank += (int)partner_u32<1>((uint32_t)rank, lane);
+      if (parts > 2) rank += (int)partner_u32<2>((uint32_t)rank, lane);
+      if (parts > 4) rank += (int)partner_u32<4>((uint32_t)rank, lane);
+      if (parts > 8) rank += (int)partner_u32<8>((uint32_t)rank, lane);
+      if (parts > 16) rank += (int)partner_u32<16>((uint32_t)rank, lane);
+      if (parts > 32) rank += (int)partner_u32<32>((uint32_t)rank, lane);
       if (part == 0 && rank < K) r.pick_w[rank] = r.p[i], r.pick_i[rank] = i;
     }
   } else {
