@@ -40,6 +40,22 @@ G4_DEV float wave_fsum(float v) {
   return pstep<1>(v);
 }
 
+// Sum over each aligned group of N lanes (N a power of two), without LDS:
+// partners at distances 1, 2, 4, ... (DPP quad permutes; at 4 the half-row
+// mirror, which after the steps at 1 and 2 pairs the two quads of every 8
+// lanes; row_ror:8; then permlane swaps), every lane of a group ending with its
+// group's sum.
+template <int N>
+G4_DEV float group_sum(float s, int lane) {
+  if constexpr (N > 1) s += __uint_as_float(partner_u32<1>(__float_as_uint(s), lane));
+  if constexpr (N > 2) s += __uint_as_float(partner_u32<2>(__float_as_uint(s), lane));
+  if constexpr (N > 4) s += __uint_as_float(partner_u32<4>(__float_as_uint(s), lane));
+  if constexpr (N > 8) s += __uint_as_float(partner_u32<8>(__float_as_uint(s), lane));
+  if constexpr (N > 16) s += __uint_as_float(partner_u32<16>(__float_as_uint(s), lane));
+  if constexpr (N > 32) s += __uint_as_float(partner_u32<32>(__float_as_uint(s), lane));
+  return s;
+}
+
 G4_DEV float wave_jmax(float v) {  // every lane: the wave's maximum (butterfly without LDS)
   const int lane = threadIdx.x & 63;
   v = jmax(v, __uint_as_float(partner_u32<32>(__float_as_uint(v), lane)));
@@ -119,9 +135,7 @@ __global__ __launch_bounds__(256) void k_att_part(AttArgs a) {
           s = __builtin_fmaf(qv[g][4 * j + 2], kk[u][j].z, s);
           s = __builtin_fmaf(qv[g][4 * j + 3], kk[u][j].w, s);
         }
-#pragma unroll
-        for (int m = 1; m < LS; m <<= 1) s += __shfl_xor(s, m, 64);
-        d[g] = s;
+        d[g] = group_sum<LS>(s, lane);
       }
       if (ql == 0)
 #pragma unroll
