@@ -51,21 +51,21 @@ Q8_0, Q4_0, Q4_K = 8, 2, 12
 # Recorded in profiles/hbm_traffic_fetch_write_size.md (same command and kernels).
 # "name:part" keys give the other separately timed launches of a step.
 TRAFFIC_BYTES = {
-    "q4_0_ffn_decode_token": 19202816,
+    "q4_0_ffn_decode_token": 19175168,
     "q4_0_ffn_decode_token:down": 9825152,
-    "q8_0_matvec_2048x2048": 4633472,
-    "q8_0_lm_head_262144x2048_argmax": 572094112,
+    "q8_0_matvec_2048x2048": 4629376,
+    "q8_0_lm_head_262144x2048_argmax": 572104096,
     "q4_k_batched_8192x2048_m1": 9658240,
     "q4_k_batched_8192x2048_m8": 10354432,
     "q4_k_batched_8192x2048_m32": 12713728,
     "q4_k_batched_8192x2048_m64": 15859456,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40024256,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 546615680,
-    "q5_k_matvec_8192x2048": 11775872,
-    "q6_k_matvec_8192x2048": 14131968,
-    "q4_0_ffn_block_decode_token": 29148800,
-    "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572333824,
-    "attention_decode_h16_kv8_d256_len8192": 136787136,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40020160,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 547989664,
+    "q5_k_matvec_8192x2048": 11763584,
+    "q6_k_matvec_8192x2048": 14137088,
+    "q4_0_ffn_block_decode_token": 29134464,
+    "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572357472,
+    "attention_decode_h16_kv8_d256_len8192": 136771584,
 }
 
 
