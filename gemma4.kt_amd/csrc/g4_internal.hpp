@@ -98,6 +98,33 @@ bool tok_ok(int type, const TokArgs &a);
 int64_t tok_scratch_floats(const TokArgs &a, const DevInfo &dev);
 hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_t stream);
 
+// Routed experts of a multi-token MoE call on the matrix cores, grouped by
+// expert (Q4_K): pair p = (token p / x_div, slot p % x_div) with expert ids[p]
+// reads x + (p / x_div) * x_stride and writes y + p * y_stride.  gate_up: rows
+// r < rows of the gate (base0) and up (base1) matrices, y[r] = gelu(gate) * up;
+// otherwise rows r < rows from base0, y[r] = row r . x.  Expert e's matrices
+// start expert_stride elements after expert e - 1's.  Pairs whose id is outside
+// [0, n_experts) get zero rows.
+struct MoeGrpArgs {
+  const uint8_t *W;
+  int64_t base0;
+  int64_t base1;
+  int64_t row_stride;
+  int64_t expert_stride;
+  const int32_t *ids;
+  int32_t S;  // (token, slot) pairs
+  int32_t n_experts;
+  int32_t rows;
+  int32_t dim1;
+  const float *x;
+  int64_t x_stride;
+  int32_t x_div;
+  float *y;
+  int64_t y_stride;
+};
+bool moe_grp_ok(int type, const MoeGrpArgs &a);
+hipError_t launch_moe_grp(int type, bool gate_up, const MoeGrpArgs &a, const DevInfo &dev, hipStream_t stream);
+
 // Plain matvec of rows of 65..256 chunks (g4_wide.hip): the columns split over
 // the waves of a workgroup.  wide_ok: the launch takes it (EPI_STORE, no ids,
 // no fused norm or routing, 64-element aligned rows of the row-stream formats).
@@ -107,6 +134,8 @@ hipError_t launch_wide(int type, const RowsArgs &a, int segments, hipStream_t st
 hipError_t launch_dequant(int type, const uint8_t *W, int64_t offset, int64_t n, float *out, hipStream_t stream);
 hipError_t launch_argmax(const float *v, int32_t n, float *part_val, int32_t *part_idx, int32_t *out,
                          const DevInfo &dev, hipStream_t stream);
+// launch_route takes up to this many experts per token.
+constexpr int ROUTE_LAUNCH_MAX_E = 1024;
 hipError_t launch_route(const float *logits, int32_t T, int32_t n_experts, int32_t k, int32_t renorm,
                         const float *expert_scale, int32_t *ids, float *weights, hipStream_t stream);
 // Down projection and weighted sum of the routed experts in one launch for few

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void k_argmax_final(const float *pv, const int
 // fp32 divide), top-k of Llama.kt:275-293 (strict >, ties to the lowest index,
 // chosen entries masked to -inf), optional renormalisation (fp32 sum in k
 // order) and expert scale.  Used by k_route and by the routed gate+up launch.
-constexpr int ROUTE_MAX_E = 1024;       // k_route
+constexpr int ROUTE_MAX_E = ROUTE_LAUNCH_MAX_E;  // k_route
 constexpr int ROUTE_FUSED_MAX_E = 256;  // routing inside the gate+up launch
 constexpr int ROUTE_FILTER_MAX_K = 32;  // top-k through the candidate filter up to this k
 

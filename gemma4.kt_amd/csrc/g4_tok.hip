@@ -528,4 +528,251 @@ hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------ grouped MoE ----
+// The routed experts of a multi-token MoE call (Llama.kt:300-337 runs expert
+// ids[p] on the x of token p / K for every (token, slot) pair p), grouped by
+// expert: each expert's Q4_K weights are read and unpacked once for all of its
+// pairs, on the matrix cores with the exact 3 x bf16 products of k_tok_q4k.
+//
+// Workgroup (x, e) takes expert e's pairs (ids[p] == e, in pair order) four at
+// a time.  Their x rows are split into bf16 parts once, into LDS, in the MFMA
+// operand layout.  Pair slot t fills A rows 4t .. 4t + 3 (the same x four
+// times), so C row 4j, the first of the four outputs lane (j, n) holds, is pair
+// slot j's: every lane ends with one output per weight row, with no shuffle.
+// Each wave walks units of two 16-row tiles (the gate and the up tile of the
+// same rows, or two consecutive tiles) over all the columns, 128 at a time
+// (four 32-weight sub-blocks, one fp32 MFMA for their (8 d*sc - dmin*m) sum(x)
+// terms).  The sums stay in registers, so there is no cross-wave reduction.
+// Workgroups (x, n_experts) write the zero rows of pairs whose id is out of
+// range.
+constexpr int MG_WPB = 4;        // waves per workgroup
+constexpr int MG_UPW = 2;        // units per wave
+constexpr int MG_DEPTH = 2;      // chunks of weights in registers (MG_DEPTH - 1 in flight)
+constexpr int MG_MAX_S = 4096;   // pairs every workgroup scans
+constexpr int MG_MAX_DIM1 = 2560;  // columns: the LDS operands of four pairs fit in 64 KB
+
+// sc and m of sub-blocks 4 hq .. 4 hq + 3 for a per-lane hq, in bytes 0..3
+G4_DEV void scale_min_quad_sel(const u32x4 &H, int hq, uint32_t &scq, uint32_t &mq) {
+  const uint32_t s0 = H.y & 0x3F3F3F3Fu, m0 = H.z & 0x3F3F3F3Fu;
+  const uint32_t s1 = (H.w & 0x0F0F0F0Fu) | ((H.y >> 2) & 0x30303030u);
+  const uint32_t m1 = ((H.w >> 4) & 0x0F0F0F0Fu) | ((H.z >> 2) & 0x30303030u);
+  scq = hq ? s1 : s0;
+  mq = hq ? m1 : m0;
+}
+
+static size_t mg_lds_bytes(int dim1) {
+  const size_t nsb = (size_t)(dim1 >> 5);
+  return nsb * 3 * 16 * sizeof(u32x4) + nsb * 4 * sizeof(float);
+}
+
+template <bool GU>
+__global__ __launch_bounds__(MG_WPB * 64) void k_moe_grp(MoeGrpArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char mg_lds[];
+  __shared__ int pl[4];          // the pass's pairs (-1: none)
+  __shared__ int wcnt[MG_WPB];   // matches per wave in a scan step
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, j = lane >> 4;
+  const int e = blockIdx.y;
+  const bool zero_rows = e == a.n_experts;
+  const int NSB = a.dim1 >> 5, NCH = a.dim1 >> 7;
+  u32x4 *xp = (u32x4 *)mg_lds;                                     // [NSB][3 parts][4 K-slices][4 slots]
+  float *xs = (float *)(mg_lds + (size_t)NSB * 3 * 16 * sizeof(u32x4));  // [NSB][4 slots]
+  constexpr int UR = GU ? 16 : 32;  // rows per unit
+  const int units = (a.rows + UR - 1) / UR;
+  const int u_lo = (int)blockIdx.x * MG_UPW * MG_WPB, u_hi = min(units, u_lo + MG_UPW * MG_WPB);
+  const int64_t eoff = zero_rows ? 0 : (int64_t)e * a.expert_stride;
+
+  // pairs of rank 4 pass .. 4 pass + 3 among this workgroup's into pl; returns
+  // the number of its pairs (the same in every thread)
+  auto scan = [&](int pass) {
+    if (tid < 4) pl[tid] = -1;
+    int total = 0;
+    for (int p0 = 0; p0 < a.S; p0 += MG_WPB * 64) {
+      const int p = p0 + tid;
+      bool m = false;
+      if (p < a.S) {
+        const int id = a.ids[p];
+        m = zero_rows ? (id < 0 || id >= a.n_experts) : id == e;
+      }
+      const uint64_t b = __builtin_amdgcn_ballot_w64(m);
+      if (lane == 0) wcnt[wid] = __builtin_popcountll(b);
+      __syncthreads();
+      int before = total, all = 0;
+#pragma unroll
+      for (int w = 0; w < MG_WPB; ++w) {
+        before += w < wid ? wcnt[w] : 0;
+        all += wcnt[w];
+      }
+      const int rank = before + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+      if (m && rank >= 4 * pass && rank < 4 * pass + 4) pl[rank - 4 * pass] = p;
+      total += all;
+      __syncthreads();  // wcnt is rewritten next step; pl is complete after the last
+    }
+    return total;
+  };
+
+  for (int pass = 0;; ++pass) {
+    if (pass > 0) __syncthreads();  // every wave has stored the previous pass's rows
+    const int total = scan(pass);
+    const int cnt = min(4, total - 4 * pass);
+    if (cnt <= 0) return;
+    if (zero_rows) {
+      for (int i = tid; i < cnt * (u_hi - u_lo) * UR; i += MG_WPB * 64) {
+        const int t = i / ((u_hi - u_lo) * UR), r = u_lo * UR + i % ((u_hi - u_lo) * UR);
+        if (r < a.rows) a.y[(int64_t)pl[t] * a.y_stride + r] = 0.f;
+      }
+      continue;
+    }
+
+    // x of the pass's pairs in 8-column pieces (slot t, sub-block s, K-slice q):
+    // the three bf16 parts (with the infinity guard) and, over the four
+    // K-slices of a sub-block (four adjacent lanes), the sub-block's sum
+    for (int o = tid; o < 16 * NSB; o += MG_WPB * 64) {
+      const int t = o / (4 * NSB), rem = o - t * 4 * NSB, s = rem >> 2, q = rem & 3;
+      const int p = pl[t];
+      float v[8];
+      if (p >= 0) {
+        const u32x4a4 *src = (const u32x4a4 *)(a.x + (int64_t)(p / a.x_div) * a.x_stride + 32 * s + 8 * q);
+        const u32x4a4 lo = src[0], hi = src[1];
+        v[0] = __uint_as_float(lo.x), v[1] = __uint_as_float(lo.y), v[2] = __uint_as_float(lo.z);
+        v[3] = __uint_as_float(lo.w), v[4] = __uint_as_float(hi.x), v[5] = __uint_as_float(hi.y);
+        v[6] = __uint_as_float(hi.z), v[7] = __uint_as_float(hi.w);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.f;
+      }
+      bf16x8 p1, p2, p3;
+      split3<true>(v, p1, p2, p3);
+      u32x4 *d = xp + (size_t)s * 48 + q * 4 + t;
+      d[0] = __builtin_bit_cast(u32x4, p1);
+      d[16] = __builtin_bit_cast(u32x4, p2);
+      d[32] = __builtin_bit_cast(u32x4, p3);
+      float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+      sum = pstep<1>(sum);
+      sum = pstep<2>(sum);
+      if (q == 0) xs[s * 4 + t] = sum;
+    }
+    __syncthreads();
+
+    const int slot = n >> 2;  // the pair slot whose x this lane's A rows carry
+    const int pj = pl[j];     // the pair of this lane's outputs (-1: none)
+    for (int k = 0; k < MG_UPW; ++k) {
+      const int u = u_lo + k * MG_WPB + wid;
+      if (u >= u_hi) break;  // wave-uniform
+      // this lane's row of the two tiles; rows past the end read the tensor's
+      // first super-blocks (in bounds, never stored)
+      const int r0 = u * UR + n, r1 = GU ? r0 : r0 + 16;
+      const bool ok0 = r0 < a.rows, ok1 = r1 < a.rows;
+      const int64_t E0 = ok0 ? eoff + a.base0 + (int64_t)r0 * a.row_stride : 0;
+      const int64_t E1 = ok1 ? eoff + (GU ? a.base1 : a.base0) + (int64_t)r1 * a.row_stride : 0;
+      const uint8_t *sb0 = a.W + (E0 >> 8) * 144, *sb1 = a.W + (E1 >> 8) * 144;
+      const int h0 = (int)(E0 >> 7) & 1, h1 = (int)(E1 >> 7) & 1;
+      // chunk c of a row starting at half h: super-block (h + c) / 2, half (h + c) % 2
+      auto load = [&](int c, const uint8_t *sb, int h, u32x4 &H, u32x2a4 &Q0, u32x2a4 &Q1) {
+        const uint8_t *b = sb + ((h + c) >> 1) * 144;
+        const int hq = (h + c) & 1;
+        H = *(const u32x4 *)b;
+        Q0 = *(const u32x2a4 *)(b + 16 + 64 * hq + 8 * j);
+        Q1 = *(const u32x2a4 *)(b + 48 + 64 * hq + 8 * j);
+      };
+      // the weights of MG_DEPTH chunks: MG_DEPTH - 1 load while one multiplies
+      struct Wt {
+        u32x4 H0, H1;
+        u32x2a4 Q0[2], Q1[2];
+      };
+      auto load2 = [&](int c, Wt &w) {
+        c = min(c, NCH - 1);  // past the end: the last chunk again (in bounds, unused)
+        load(c, sb0, h0, w.H0, w.Q0[0], w.Q0[1]);
+        load(c, sb1, h1, w.H1, w.Q1[0], w.Q1[1]);
+      };
+      Wt W[MG_DEPTH];
+#pragma unroll
+      for (int i = 0; i + 1 < MG_DEPTH; ++i) load2(i, W[i]);
+      f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+
+      // one tile's four sub-blocks of chunk c: scales, unpacked nibbles and products
+      auto tile = [&](int c, int h, const u32x4 &H, const u32x2a4 (&Q)[2], const bf16x8 (&A)[4][3], float xsA,
+                      f32x4 &acc) {
+        const int hq = (h + c) & 1;
+        uint32_t scq, mq;
+        scale_min_quad_sel(H, hq, scq, mq);
+        const float dq = h2f(H.x & 0xFFFFu) * 0.0625f, dmin = h2f(H.x >> 16);
+        const float scj = (float)((scq >> (8 * j)) & 0xFFu), mj = (float)((mq >> (8 * j)) & 0xFFu);
+        const float cj = __builtin_fmaf(128.f, dq * scj, -(dmin * mj));
+        f32x4 P[4];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const uint32_t w0 = Q[g].x, w1 = Q[g].y;
+          const bf16x8 bl = nibbles_bf16(opaque(lo_nibbles_s16(w0)), opaque(lo_nibbles_s16(w1)));
+          const bf16x8 bh = nibbles_bf16(opaque(hi_nibbles_s16(w0)), opaque(hi_nibbles_s16(w1)));
+          P[2 * g] = P[2 * g + 1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int p = 0; p < 3; ++p) {
+            P[2 * g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[2 * g][p], bl, P[2 * g], 0, 0, 0);
+            P[2 * g + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[2 * g + 1][p], bh, P[2 * g + 1], 0, 0, 0);
+          }
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xsA, cj, acc, 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[0] = __builtin_fmaf(dq * ubyte(scq, s), P[s][0], acc[0]);
+      };
+
+      // chunk c's products for both tiles (the x operands read once)
+      auto chunk = [&](int c, const Wt &w) {
+        bf16x8 A[4][3];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int p = 0; p < 3; ++p)
+            A[s][p] = __builtin_bit_cast(bf16x8, xp[(size_t)(4 * c + s) * 48 + p * 16 + j * 4 + slot]);
+        const float xsA = xs[(4 * c + j) * 4 + slot];
+        tile(c, h0, w.H0, w.Q0, A, xsA, acc0);
+        tile(c, h1, w.H1, w.Q1, A, xsA, acc1);
+      };
+      // unrolled by the ring size, so every buffer index is a constant
+      for (int c0 = 0; c0 < NCH; c0 += MG_DEPTH) {
+#pragma unroll
+        for (int i = 0; i < MG_DEPTH; ++i) {
+          if (c0 + i >= NCH) break;  // wave-uniform
+          load2(c0 + i + MG_DEPTH - 1, W[(i + MG_DEPTH - 1) % MG_DEPTH]);
+          chunk(c0 + i, W[i]);
+        }
+      }
+      if (pj >= 0) {
+        float *yp = a.y + (int64_t)pj * a.y_stride;
+        if constexpr (GU) {
+          if (ok0) yp[r0] = gelu_ref(acc0[0]) * acc1[0];
+        } else {
+          if (ok0) yp[r0] = acc0[0];
+          if (ok1) yp[r1] = acc1[0];
+        }
+      }
+    }
+  }
+}
+
+bool moe_grp_ok(int type, const MoeGrpArgs &a) {
+  if (type != T_Q4_K) return false;
+  if (a.dim1 <= 0 || a.dim1 % 128 != 0 || a.dim1 > MG_MAX_DIM1) return false;
+  if (a.base0 % 128 != 0 || a.base1 % 128 != 0 || a.row_stride % 128 != 0 || a.expert_stride % 128 != 0)
+    return false;
+  return a.S >= 1 && a.S <= MG_MAX_S && a.rows >= 1 && a.x_div >= 1 && a.n_experts >= 1;
+}
+
+hipError_t launch_moe_grp(int type, bool gate_up, const MoeGrpArgs &a, const DevInfo &dev, hipStream_t s) {
+  (void)dev;
+  if (!moe_grp_ok(type, a)) return hipErrorNotSupported;
+  const int ur = gate_up ? 16 : 32;
+  const int units = (a.rows + ur - 1) / ur;
+  const dim3 grid((unsigned)((units + MG_UPW * MG_WPB - 1) / (MG_UPW * MG_WPB)), (unsigned)a.n_experts + 1);
+  const size_t lds = mg_lds_bytes(a.dim1);
+  if (gate_up)
+    hipLaunchKernelGGL(k_moe_grp<true>, grid, dim3(MG_WPB * 64), lds, s, a);
+  else
+    hipLaunchKernelGGL(k_moe_grp<false>, grid, dim3(MG_WPB * 64), lds, s, a);
+  return hipGetLastError();
+}
+
 }  // namespace g4

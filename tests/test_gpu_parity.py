@@ -567,6 +567,52 @@ def test_moe_batch_equals_tokens_alone(g4, ctx, oracle, fmt):
     assert_dots(Yb.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe batch")
 
 
+@pytest.mark.parametrize("case", ["t64", "t80_e8", "ff384", "nonfinite"])
+def test_moe_grouped_by_expert(g4, ctx, oracle, case):
+    """Calls of 64 or more Q4_K tokens run each expert once for all of its (token,
+    slot) pairs on the matrix cores (3 x bf16 products, fp32 sums).  The routed
+    and the id-taking entry points give the same bits; every output is within the
+    bound; a token alone (row kernels) rounds differently but shares the bound.
+    t80_e8: ten pairs per expert on average, so experts take up to four passes of
+    four pairs; ff384: down rows of 384 columns, every second one starting half
+    way into a super-block; nonfinite: +inf, NaN and -inf activations reach only
+    their own tokens."""
+    announce("moe grouped %s" % case)
+    E, D, FF, K, T = 32, 512, 256, 4, 64
+    if case == "t80_e8":
+        E, K, T = 8, 1, 80
+    elif case == "ff384":
+        FF = 384
+    gu = synth.q4_k(61, "gu" + case, E * 2 * FF * D)
+    dn = synth.q4_k(61, "dn" + case, E * D * FF)
+    lg = synth.activations(61, "lg" + case, T * E).reshape(T, E)
+    X = synth.activations(61, "X" + case, T * D).reshape(T, D)
+    bad = {}
+    if case == "nonfinite":
+        X[3, 7] = np.inf
+        X[10, 300] = np.nan
+        X[40, D - 1] = -np.inf
+        bad = {3, 10, 40}
+    wgu = upload(g4, ctx, Q4_K, gu, E * 2 * FF * D)
+    wdn = upload(g4, ctx, Q4_K, dn, E * D * FF)
+    Yr, idr, wr = g4.moe_routed(ctx, wgu, wdn, X, lg, K, True, D, FF)
+    rids, rw = oracle.route(lg, K, True)
+    assert np.array_equal(idr, rids) and same_bits(wr, rw)
+    if case == "t80_e8":
+        assert max(np.bincount(idr.reshape(-1))) > 12
+    Y = g4.moe(ctx, wgu, wdn, X, rids, rw, D, FF)
+    assert same_bits(Yr, Y)
+    y64, bound = oracle.moe_exact(Q4_K, gu, Q4_K, dn, X, rids, rw, D, FF)
+    for t in range(T):
+        if t in bad:
+            assert not np.any(np.isfinite(Y[t])), t
+        else:
+            assert_dots(Y[t], y64[t], bound[t], "moe grouped %s token %d" % (case, t))
+    for t in (0, T - 1):
+        Y1, _, _ = g4.moe_routed(ctx, wgu, wdn, X[t:t + 1], lg[t:t + 1], K, True, D, FF)
+        assert_dots(Y1[0], y64[t], bound[t], "moe token %d alone" % t)
+
+
 def test_moe_routed_dev_calls(g4, ctx, oracle):
     """The device entry point on resident buffers, twice in a row with fewer tokens
     the second time: ids, weights and Y of each call match the host entry point."""
@@ -594,6 +640,45 @@ def test_moe_routed_dev_calls(g4, ctx, oracle):
         assert np.array_equal(d_ids.cpu().numpy(), idh), call
         assert same_bits(d_w.cpu().numpy(), wh), call
         assert same_bits(d_Y.cpu().numpy(), Yh), call
+
+
+@pytest.mark.parametrize("tokens", [1, 16, 64])
+def test_moe_dev_out_of_range_ids(g4, ctx, oracle, tokens):
+    """g4_moe_dev cannot check device ids: a pair whose id is outside [0, E) gets
+    zero gate/up and down rows, so it adds w * 0 to its token's sum.  One token
+    (down and weighted sum in one launch), 16 tokens (per-pair launches) and 64
+    tokens (experts grouped on the matrix cores)."""
+    import torch
+    announce("moe dev out-of-range ids T=%d" % tokens)
+    E, D, FF, K, T = 16, 512, 256, 4, tokens
+    gu = synth.q4_k(59, "gu", E * 2 * FF * D)
+    dn = synth.q4_k(59, "dn", E * D * FF)
+    lg = synth.activations(59, "lg%d" % T, T * E).reshape(T, E)
+    X = synth.activations(59, "X%d" % T, T * D).reshape(T, D)
+    wgu = upload(g4, ctx, Q4_K, gu, E * 2 * FF * D)
+    wdn = upload(g4, ctx, Q4_K, dn, E * D * FF)
+    ids, gw = g4.moe_route(ctx, lg, K, True)
+    bad = ids.copy()
+    bad[0, 1] = -1
+    bad[T - 1, K - 1] = E
+    if T > 2:
+        bad[T // 2, 0] = 1 << 30
+    d_Y = torch.full((T, D), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    try:
+        g4.moe_dev(ctx, wgu, wdn, torch.from_numpy(X).cuda(), T, D, FF, torch.from_numpy(bad).cuda(),
+                   torch.from_numpy(gw).cuda(), K, d_Y)
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_stream(None)
+    Y = d_Y.cpu().numpy()
+    # the oracle with those slots' weights zeroed (their ids made valid)
+    ids0, w0 = bad.copy(), gw.copy()
+    off = (bad < 0) | (bad >= E)
+    ids0[off] = 0
+    w0[off] = 0.0
+    y64, bound = oracle.moe_exact(Q4_K, gu, Q4_K, dn, X, ids0, w0, D, FF)
+    assert_dots(Y.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe dev bad ids T=%d" % T)
 
 
 def test_moe_repeated_calls(g4, ctx, oracle):
