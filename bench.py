@@ -308,10 +308,15 @@ class MoeQ4_K(Workload):
         import synth
         self.T = tokens
         self.name = "moe_q4_k_128x(2816x2048+2048x1408)_top8_t%d" % tokens
-        # one token: the down projection and the weighted sum share a launch
-        self.dominant_name = ("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE> (routing + gate_up) + " +
-                              ("k_moe_down<FmtQ4_K, 32, 8> (down + weighted sum)" if tokens == 1 else
-                               "k_rows<FmtQ4_K, 8, 3, XL> (down) + k_moe_combine"))
+        # one token: the down projection and the weighted sum share a launch; 64 or
+        # more tokens: a routing launch, then the experts grouped on the matrix cores
+        if tokens >= 64:
+            self.dominant_name = ("g4_moe_routed: k_route + k_moe_grp<gate_up> + k_moe_grp<down> (experts grouped "
+                                  "on the matrix cores) + k_moe_combine")
+        else:
+            self.dominant_name = ("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE> (routing + gate_up) + " +
+                                  ("k_moe_down<FmtQ4_K, 32, 8> (down + weighted sum)" if tokens == 1 else
+                                   "k_rows<FmtQ4_K, 8, 3, XL> (down) + k_moe_combine"))
         base = synth.moe_q4_k(tokens)
         E, D, FF, K = base["n_experts"], base["dim"], base["ff"], base["k"]
         self.E, self.D, self.FF, self.K = E, D, FF, K
@@ -837,8 +842,8 @@ def main():
     specs = args.workload.split(",")
     if args.all:
         specs = ["q4_0_ffn", "q8_0_matvec", "q8_0_lm_head", "q4_k_batched:1", "q4_k_batched:8",
-                 "q4_k_batched:32", "q4_k_batched:64", "moe:1", "moe:16", "q5_k_matvec", "q6_k_matvec",
-                 "q4_0_ffn_block", "q8_0_lm_head_cap", "attention:8192"]
+                 "q4_k_batched:32", "q4_k_batched:64", "moe:1", "moe:16", "moe:128", "q5_k_matvec",
+                 "q6_k_matvec", "q4_0_ffn_block", "q8_0_lm_head_cap", "attention:8192"]
     if args.steps < 1:
         raise SystemExit("--steps must be at least 1")
     default = not args.all and args.workload == "q4_0_ffn"

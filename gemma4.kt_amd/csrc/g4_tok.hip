@@ -534,22 +534,26 @@ hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_
 // expert: each expert's Q4_K weights are read and unpacked once for all of its
 // pairs, on the matrix cores with the exact 3 x bf16 products of k_tok_q4k.
 //
-// Workgroup (x, e) takes expert e's pairs (ids[p] == e, in pair order) four at
+// Workgroup (x, e) takes expert e's pairs (ids[p] == e, in pair order) eight at
 // a time.  Their x rows are split into bf16 parts once, into LDS, in the MFMA
-// operand layout.  Pair slot t fills A rows 4t .. 4t + 3 (the same x four
-// times), so C row 4j, the first of the four outputs lane (j, n) holds, is pair
-// slot j's: every lane ends with one output per weight row, with no shuffle.
+// operand layout.  Pair slot t fills A rows 2t and 2t + 1 (the same x twice),
+// so C rows 4j and 4j + 2, outputs 0 and 2 of the four lane (j, n) holds, are
+// pair slots 2j and 2j + 1: every lane ends with two outputs per weight row, with
+// no shuffle.
 // Each wave walks units of two 16-row tiles (the gate and the up tile of the
 // same rows, or two consecutive tiles) over all the columns, 128 at a time
 // (four 32-weight sub-blocks, one fp32 MFMA for their (8 d*sc - dmin*m) sum(x)
 // terms).  The sums stay in registers, so there is no cross-wave reduction.
 // Workgroups (x, n_experts) write the zero rows of pairs whose id is out of
 // range.
-constexpr int MG_WPB = 4;        // waves per workgroup
+constexpr int MG_TOK = 8;        // pairs per pass (MFMA rows 16 / MG_TOK per pair)
+constexpr int MG_RPS = 16 / MG_TOK, MG_NOUT = MG_TOK / 4;  // A rows per pair, outputs per lane
+constexpr int MG_SBS = 3 * 4 * MG_TOK;  // 16-byte LDS operands per sub-block: parts x K-slices x pairs
+constexpr int MG_WPB = 8;        // waves per workgroup
 constexpr int MG_UPW = 2;        // units per wave
 constexpr int MG_DEPTH = 2;      // chunks of weights in registers (MG_DEPTH - 1 in flight)
 constexpr int MG_MAX_S = 4096;   // pairs every workgroup scans
-constexpr int MG_MAX_DIM1 = 2560;  // columns: the LDS operands of four pairs fit in 64 KB
+constexpr int MG_MAX_DIM1 = 3072;  // columns: the LDS operands of eight pairs fit in 150 KB
 
 // sc and m of sub-blocks 4 hq .. 4 hq + 3 for a per-lane hq, in bytes 0..3
 G4_DEV void scale_min_quad_sel(const u32x4 &H, int hq, uint32_t &scq, uint32_t &mq) {
@@ -562,13 +566,13 @@ G4_DEV void scale_min_quad_sel(const u32x4 &H, int hq, uint32_t &scq, uint32_t &
 
 static size_t mg_lds_bytes(int dim1) {
   const size_t nsb = (size_t)(dim1 >> 5);
-  return nsb * 3 * 16 * sizeof(u32x4) + nsb * 4 * sizeof(float);
+  return nsb * MG_SBS * sizeof(u32x4) + nsb * MG_TOK * sizeof(float);
 }
 
 template <bool GU>
 __global__ __launch_bounds__(MG_WPB * 64) void k_moe_grp(MoeGrpArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char mg_lds[];
-  __shared__ int pl[4];          // the pass's pairs (-1: none)
+  __shared__ int pl[MG_TOK];     // the pass's pairs (-1: none)
   __shared__ int wcnt[MG_WPB];   // matches per wave in a scan step
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -576,17 +580,17 @@ __global__ __launch_bounds__(MG_WPB * 64) void k_moe_grp(MoeGrpArgs a) {
   const int e = blockIdx.y;
   const bool zero_rows = e == a.n_experts;
   const int NSB = a.dim1 >> 5, NCH = a.dim1 >> 7;
-  u32x4 *xp = (u32x4 *)mg_lds;                                     // [NSB][3 parts][4 K-slices][4 slots]
-  float *xs = (float *)(mg_lds + (size_t)NSB * 3 * 16 * sizeof(u32x4));  // [NSB][4 slots]
+  u32x4 *xp = (u32x4 *)mg_lds;                                       // [NSB][3 parts][4 K-slices][MG_TOK slots]
+  float *xs = (float *)(mg_lds + (size_t)NSB * MG_SBS * sizeof(u32x4));  // [NSB][MG_TOK slots]
   constexpr int UR = GU ? 16 : 32;  // rows per unit
   const int units = (a.rows + UR - 1) / UR;
   const int u_lo = (int)blockIdx.x * MG_UPW * MG_WPB, u_hi = min(units, u_lo + MG_UPW * MG_WPB);
   const int64_t eoff = zero_rows ? 0 : (int64_t)e * a.expert_stride;
 
-  // pairs of rank 4 pass .. 4 pass + 3 among this workgroup's into pl; returns
+  // pairs of rank MG_TOK pass .. MG_TOK (pass + 1) - 1 among this workgroup's into pl; returns
   // the number of its pairs (the same in every thread)
   auto scan = [&](int pass) {
-    if (tid < 4) pl[tid] = -1;
+    if (tid < MG_TOK) pl[tid] = -1;
     int total = 0;
     for (int p0 = 0; p0 < a.S; p0 += MG_WPB * 64) {
       const int p = p0 + tid;
@@ -606,7 +610,7 @@ __global__ __launch_bounds__(MG_WPB * 64) void k_moe_grp(MoeGrpArgs a) {
       }
       const int rank = before + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-      if (m && rank >= 4 * pass && rank < 4 * pass + 4) pl[rank - 4 * pass] = p;
+      if (m && rank >= MG_TOK * pass && rank < MG_TOK * (pass + 1)) pl[rank - MG_TOK * pass] = p;
       total += all;
       __syncthreads();  // wcnt is rewritten next step; pl is complete after the last
     }
@@ -616,7 +620,7 @@ __global__ __launch_bounds__(MG_WPB * 64) void k_moe_grp(MoeGrpArgs a) {
   for (int pass = 0;; ++pass) {
     if (pass > 0) __syncthreads();  // every wave has stored the previous pass's rows
     const int total = scan(pass);
-    const int cnt = min(4, total - 4 * pass);
+    const int cnt = min(MG_TOK, total - MG_TOK * pass);
     if (cnt <= 0) return;
     if (zero_rows) {
       for (int i = tid; i < cnt * (u_hi - u_lo) * UR; i += MG_WPB * 64) {
@@ -629,7 +633,7 @@ __global__ __launch_bounds__(MG_WPB * 64) void k_moe_grp(MoeGrpArgs a) {
     // x of the pass's pairs in 8-column pieces (slot t, sub-block s, K-slice q):
     // the three bf16 parts (with the infinity guard) and, over the four
     // K-slices of a sub-block (four adjacent lanes), the sub-block's sum
-    for (int o = tid; o < 16 * NSB; o += MG_WPB * 64) {
+    for (int o = tid; o < 4 * MG_TOK * NSB; o += MG_WPB * 64) {
       const int t = o / (4 * NSB), rem = o - t * 4 * NSB, s = rem >> 2, q = rem & 3;
       const int p = pl[t];
       float v[8];
@@ -645,19 +649,21 @@ __global__ __launch_bounds__(MG_WPB * 64) void k_moe_grp(MoeGrpArgs a) {
       }
       bf16x8 p1, p2, p3;
       split3<true>(v, p1, p2, p3);
-      u32x4 *d = xp + (size_t)s * 48 + q * 4 + t;
+      u32x4 *d = xp + (size_t)s * MG_SBS + q * MG_TOK + t;
       d[0] = __builtin_bit_cast(u32x4, p1);
-      d[16] = __builtin_bit_cast(u32x4, p2);
-      d[32] = __builtin_bit_cast(u32x4, p3);
+      d[4 * MG_TOK] = __builtin_bit_cast(u32x4, p2);
+      d[8 * MG_TOK] = __builtin_bit_cast(u32x4, p3);
       float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
       sum = pstep<1>(sum);
       sum = pstep<2>(sum);
-      if (q == 0) xs[s * 4 + t] = sum;
+      if (q == 0) xs[s * MG_TOK + t] = sum;
     }
     __syncthreads();
 
-    const int slot = n >> 2;  // the pair slot whose x this lane's A rows carry
-    const int pj = pl[j];     // the pair of this lane's outputs (-1: none)
+    const int slot = n / MG_RPS;  // the pair slot whose x this lane's A rows carry
+    int pj[MG_NOUT];              // the pairs of this lane's outputs (-1: none)
+#pragma unroll
+    for (int v = 0; v < MG_NOUT; ++v) pj[v] = pl[j * MG_NOUT + v];
     for (int k = 0; k < MG_UPW; ++k) {
       const int u = u_lo + k * MG_WPB + wid;
       if (u >= u_hi) break;  // wave-uniform
@@ -716,7 +722,11 @@ __global__ __launch_bounds__(MG_WPB * 64) void k_moe_grp(MoeGrpArgs a) {
         }
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xsA, cj, acc, 0, 0, 0);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc[0] = __builtin_fmaf(dq * ubyte(scq, s), P[s][0], acc[0]);
+        for (int s = 0; s < 4; ++s) {
+          const float d1 = dq * ubyte(scq, s);
+#pragma unroll
+          for (int v = 0; v < MG_NOUT; ++v) acc[v * MG_RPS] = __builtin_fmaf(d1, P[s][v * MG_RPS], acc[v * MG_RPS]);
+        }
       };
 
       // chunk c's products for both tiles (the x operands read once)
@@ -726,8 +736,8 @@ __global__ __launch_bounds__(MG_WPB * 64) void k_moe_grp(MoeGrpArgs a) {
         for (int s = 0; s < 4; ++s)
 #pragma unroll
           for (int p = 0; p < 3; ++p)
-            A[s][p] = __builtin_bit_cast(bf16x8, xp[(size_t)(4 * c + s) * 48 + p * 16 + j * 4 + slot]);
-        const float xsA = xs[(4 * c + j) * 4 + slot];
+            A[s][p] = __builtin_bit_cast(bf16x8, xp[(size_t)(4 * c + s) * MG_SBS + (p * 4 + j) * MG_TOK + slot]);
+        const float xsA = xs[(4 * c + j) * MG_TOK + slot];
         tile(c, h0, w.H0, w.Q0, A, xsA, acc0);
         tile(c, h1, w.H1, w.Q1, A, xsA, acc1);
       };
@@ -740,13 +750,15 @@ __global__ __launch_bounds__(MG_WPB * 64) void k_moe_grp(MoeGrpArgs a) {
           chunk(c0 + i, W[i]);
         }
       }
-      if (pj >= 0) {
-        float *yp = a.y + (int64_t)pj * a.y_stride;
+#pragma unroll
+      for (int v = 0; v < MG_NOUT; ++v) {
+        if (pj[v] < 0) continue;
+        float *yp = a.y + (int64_t)pj[v] * a.y_stride;
         if constexpr (GU) {
-          if (ok0) yp[r0] = gelu_ref(acc0[0]) * acc1[0];
+          if (ok0) yp[r0] = gelu_ref(acc0[v * MG_RPS]) * acc1[v * MG_RPS];
         } else {
-          if (ok0) yp[r0] = acc0[0];
-          if (ok1) yp[r1] = acc1[0];
+          if (ok0) yp[r0] = acc0[v * MG_RPS];
+          if (ok1) yp[r1] = acc1[v * MG_RPS];
         }
       }
     }
@@ -768,6 +780,13 @@ hipError_t launch_moe_grp(int type, bool gate_up, const MoeGrpArgs &a, const Dev
   const int units = (a.rows + ur - 1) / ur;
   const dim3 grid((unsigned)((units + MG_UPW * MG_WPB - 1) / (MG_UPW * MG_WPB)), (unsigned)a.n_experts + 1);
   const size_t lds = mg_lds_bytes(a.dim1);
+  const void *k = gate_up ? (const void *)k_moe_grp<true> : (const void *)k_moe_grp<false>;
+  // more than 64 KB of dynamic LDS is granted per kernel (a host-side attribute of
+  // the current device, not a stream operation)
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
   if (gate_up)
     hipLaunchKernelGGL(k_moe_grp<true>, grid, dim3(MG_WPB * 64), lds, s, a);
   else
