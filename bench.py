@@ -61,6 +61,7 @@ TRAFFIC_BYTES = {
     "q4_k_batched_8192x2048_m64": 15859456,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40020160,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 547989664,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t128": 987322060,
     "q5_k_matvec_8192x2048": 11763584,
     "q6_k_matvec_8192x2048": 14137088,
     "q4_0_ffn_block_decode_token": 29134464,
