@@ -171,7 +171,11 @@ int g4_moe_route_dev(g4_ctx *ctx, const float *d_logits, int32_t T, int32_t n_ex
  * g4_moe checks every id against the experts the weights hold
  * (G4_ERR_OUT_OF_RANGE).  g4_moe_dev cannot (the ids are device memory): a slot
  * whose id lies outside [0, n_experts) contributes nothing (its hidden vector
- * and down rows are zero), so Y is the weighted sum over the valid slots. */
+ * and down rows are zero), so Y is the weighted sum over the valid slots.
+ * Calls of 64 or more tokens with Q4_K weights (dim and ff multiples of 128 up
+ * to 3072, at most 4096 (token, slot) pairs) run the experts grouped by expert
+ * on the matrix cores: every dot within the same bound, but rounded differently
+ * from the same tokens in smaller calls. */
 int g4_moe(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *X, int32_t T,
            int32_t dim, int32_t ff, const int32_t *ids, const float *weights, int32_t k, float *Y);
 int g4_moe_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *d_X, int32_t T,
@@ -182,7 +186,8 @@ int g4_moe_dev(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down,
  * expert FFN and weighted sum of g4_moe.  logits [T x n_experts] (n_experts at
  * most the experts the weights hold); the routing is also returned in ids and
  * weights [T x k].  Up to 256 experts the routing runs inside the gate+up launch
- * (each workgroup routes its own token); above that in a launch of its own.
+ * (each workgroup routes its own token); above that, and for the calls that run
+ * the experts grouped (see g4_moe), in a launch of its own.
  * Results are identical to g4_moe_route followed by g4_moe. */
 int g4_moe_routed(g4_ctx *ctx, const g4_weight *w_gate_up, const g4_weight *w_down, const float *X, int32_t T,
                   int32_t dim, int32_t ff, const float *logits, int32_t n_experts, int32_t k, int32_t renormalize,
