@@ -642,6 +642,36 @@ def test_moe_routed_dev_calls(g4, ctx, oracle):
         assert same_bits(d_Y.cpu().numpy(), Yh), call
 
 
+@pytest.mark.parametrize("case", ["one_expert", "widest_rows", "ragged_rows", "k8_e256"])
+def test_moe_grouped_edges(g4, ctx, oracle, case):
+    """Edges of the expert-grouped calls (64+ tokens) with the ids given:
+    one_expert: all 256 pairs on one expert (32 passes of eight pairs, the other
+    experts idle); widest_rows: 3072 columns (the largest LDS operand set, 150 KB);
+    ragged_rows: workgroups left with fewer units than they hold waves for (40
+    gate+up units and 12 down units against 16 per workgroup), down rows of 640
+    columns (2.5 super-blocks); k8_e256: 256 experts, eight slots per token."""
+    announce("moe grouped edge %s" % case)
+    E, D, FF, K, T = 16, 512, 256, 4, 64
+    if case == "widest_rows":
+        E, D, FF, K = 4, 3072, 128, 2
+    elif case == "ragged_rows":
+        D, FF = 384, 640
+    elif case == "k8_e256":
+        E, D, FF, K = 256, 256, 128, 8
+    gu = synth.q4_k(62, "gu" + case, E * 2 * FF * D)
+    dn = synth.q4_k(62, "dn" + case, E * D * FF)
+    X = synth.activations(62, "X" + case, T * D).reshape(T, D)
+    lg = synth.activations(62, "lg" + case, T * E).reshape(T, E)
+    ids, gw = oracle.route(lg, K, True)
+    if case == "one_expert":
+        ids = np.full((T, K), 3, np.int32)
+    wgu = upload(g4, ctx, Q4_K, gu, E * 2 * FF * D)
+    wdn = upload(g4, ctx, Q4_K, dn, E * D * FF)
+    Y = g4.moe(ctx, wgu, wdn, X, ids, gw, D, FF)
+    y64, bound = oracle.moe_exact(Q4_K, gu, Q4_K, dn, X, ids, gw, D, FF)
+    assert_dots(Y.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe grouped %s" % case)
+
+
 @pytest.mark.parametrize("tokens", [1, 16, 64])
 def test_moe_dev_out_of_range_ids(g4, ctx, oracle, tokens):
     """g4_moe_dev cannot check device ids: a pair whose id is outside [0, E) gets
