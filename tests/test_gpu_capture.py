@@ -92,6 +92,43 @@ def test_replays_survive_a_later_scratch_regrowth(g4, moe_weights):
         c.close()
 
 
+def test_grouped_moe_replays(g4, moe_weights):
+    """A call of 96 tokens runs the experts grouped by expert: a routing launch, two
+    grouped launches (their LDS size granted per launch by a host-side kernel
+    attribute, legal under capture) and the combine.  Captured once and replayed
+    three times, with eager grouped and per-pair calls between the replays: every
+    replay gives the eager bits."""
+    announce("capture: grouped MoE replays")
+    mw = moe_weights
+    c = g4.Context(0)
+    stream = torch.cuda.Stream()
+    try:
+        big = _io(mw, 96, 5)
+        small = _io(mw, 4, 6)
+        _moe(g4, c, mw, 96, big)  # eager: sizes the scratch
+        _moe(g4, c, mw, 4, small)
+        torch.cuda.synchronize()
+        want, want_ids, want_w = big[4].clone(), big[2].clone(), big[3].clone()
+        want_small = small[4].clone()
+        big[4].fill_(float("nan"))
+        big[2].fill_(-1)
+        g = _capture(c, stream, lambda: _moe(g4, c, mw, 96, big))
+        for rep in range(3):
+            big[4].fill_(float("nan"))
+            big[2].fill_(-1)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(big[4], want), "replay %d" % rep
+            assert torch.equal(big[2], want_ids) and torch.equal(big[3], want_w), "replay %d" % rep
+            _moe(g4, c, mw, 4, small)
+            torch.cuda.synchronize()
+            assert torch.equal(small[4], want_small)
+    finally:
+        torch.cuda.synchronize()
+        c.close()
+
+
 def test_growth_under_capture_is_refused_and_reserve_fixes_it(g4, moe_weights):
     announce("capture: growth refused, then reserved")
     mw = moe_weights

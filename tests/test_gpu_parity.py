@@ -567,7 +567,7 @@ def test_moe_batch_equals_tokens_alone(g4, ctx, oracle, fmt):
     assert_dots(Yb.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe batch")
 
 
-@pytest.mark.parametrize("case", ["t64", "t80_e8", "ff384", "nonfinite"])
+@pytest.mark.parametrize("case", ["t64", "t80_e8", "ff384", "nonfinite", "ref_gates"])
 def test_moe_grouped_by_expert(g4, ctx, oracle, case):
     """Calls of 64 or more Q4_K tokens run each expert once for all of its (token,
     slot) pairs on the matrix cores (3 x bf16 products, fp32 sums).  The routed
@@ -576,9 +576,13 @@ def test_moe_grouped_by_expert(g4, ctx, oracle, case):
     t80_e8: ten pairs per expert on average, so experts take up to four passes of
     four pairs; ff384: down rows of 384 columns, every second one starting half
     way into a super-block; nonfinite: +inf, NaN and -inf activations reach only
-    their own tokens."""
+    their own tokens; ref_gates: un-renormalised gates times a per-expert down
+    scale (Llama.kt:300-337)."""
     announce("moe grouped %s" % case)
     E, D, FF, K, T = 32, 512, 256, 4, 64
+    renorm, scale = True, None
+    if case == "ref_gates":
+        renorm, scale = False, np.linspace(0.25, 2.0, E).astype(np.float32)
     if case == "t80_e8":
         E, K, T = 8, 1, 80
     elif case == "ff384":
@@ -595,8 +599,8 @@ def test_moe_grouped_by_expert(g4, ctx, oracle, case):
         bad = {3, 10, 40}
     wgu = upload(g4, ctx, Q4_K, gu, E * 2 * FF * D)
     wdn = upload(g4, ctx, Q4_K, dn, E * D * FF)
-    Yr, idr, wr = g4.moe_routed(ctx, wgu, wdn, X, lg, K, True, D, FF)
-    rids, rw = oracle.route(lg, K, True)
+    Yr, idr, wr = g4.moe_routed(ctx, wgu, wdn, X, lg, K, renorm, D, FF, scale)
+    rids, rw = oracle.route(lg, K, renorm, scale)
     assert np.array_equal(idr, rids) and same_bits(wr, rw)
     if case == "t80_e8":
         assert max(np.bincount(idr.reshape(-1))) > 12
@@ -609,7 +613,7 @@ def test_moe_grouped_by_expert(g4, ctx, oracle, case):
         else:
             assert_dots(Y[t], y64[t], bound[t], "moe grouped %s token %d" % (case, t))
     for t in (0, T - 1):
-        Y1, _, _ = g4.moe_routed(ctx, wgu, wdn, X[t:t + 1], lg[t:t + 1], K, True, D, FF)
+        Y1, _, _ = g4.moe_routed(ctx, wgu, wdn, X[t:t + 1], lg[t:t + 1], K, renorm, D, FF, scale)
         assert_dots(Y1[0], y64[t], bound[t], "moe token %d alone" % t)
 
 
