@@ -309,9 +309,9 @@ class MoeQ4_K(Workload):
         import synth
         self.T = tokens
         self.name = "moe_q4_k_128x(2816x2048+2048x1408)_top8_t%d" % tokens
-        # one token: the down projection and the weighted sum share a launch; 64 or
+        # one token: the down projection and the weighted sum share a launch; 40 or
         # more tokens: a routing launch, then the experts grouped on the matrix cores
-        if tokens >= 64:
+        if tokens >= 40:
             self.dominant_name = ("g4_moe_routed: k_route + k_moe_grp<gate_up> + k_moe_grp<down> (experts grouped "
                                   "on the matrix cores) + k_moe_combine")
         else:

@@ -473,10 +473,11 @@ int check_moe(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t T
 // Routing done inside the gate+up launch (g4_moe_routed*): the router logits in,
 // the ids and weights it stores out.
 // Calls of at least this many tokens run the experts grouped (launch_moe_grp):
-// measured on the 128-expert top-8 shape, the grouped launches are 15%, 36% and
-// 47% faster than the per-pair ones at 64, 128 and 256 tokens, and slower at 32
-// (1.2x) and 16 (2.1x), where an expert has 1.6 pairs on average.
-constexpr int32_t MOE_GROUPED_MIN_T = 64;
+// measured on the 128-expert top-8 shape, the grouped launches are 3%, 13%, 17%,
+// 36% and 47% faster than the per-pair ones at 40, 48, 56, 128 and 256 tokens,
+// even at 33, and slower at 24 (1.4x) and 16 (2.1x), where an expert has 1.6
+// pairs on average.
+constexpr int32_t MOE_GROUPED_MIN_T = 40;
 
 struct MoeRoute {
   const float *d_logits;

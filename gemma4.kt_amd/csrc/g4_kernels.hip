@@ -1041,7 +1041,21 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
   // stream (the 570 MB LM head) was measured slower, and the small launches
   // never reach the cap
   constexpr int WG_CAP = 8 / WPB;
-  const int64_t cap = cu * (res < WG_CAP ? res : WG_CAP) / segs;
+  const int64_t slots = cu * (res < WG_CAP ? res : WG_CAP);
+  int64_t cap = slots / segs;
+  // When the segments do not divide the resident workgroups evenly, more
+  // workgroups per segment can even out the CUs: b workgroups per segment leave
+  // the busiest CU ceil(b * segs / cu) of them, 1/b segment each (320 MoE pairs
+  // on 256 CUs: two whole segments on some CUs at b = 1, 1.25 at b = 4).  The
+  // smallest b up to four times the resident share that loads the busiest CU
+  // least.
+  if (cap >= 1 && slots % segs != 0) {
+    auto busiest = [&](int64_t b) { return (double)((b * segs + cu - 1) / cu) / (double)b; };
+    int64_t best = cap;
+    for (int64_t b = cap + 1; b <= 4 * cap && b <= blocks; ++b)
+      if (busiest(b) < busiest(best)) best = b;
+    cap = best;
+  }
   if (blocks > cap) blocks = cap;
   if (blocks > n_tiles) blocks = n_tiles;
   if (blocks < 1) blocks = 1;

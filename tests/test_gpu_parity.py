@@ -569,7 +569,7 @@ def test_moe_batch_equals_tokens_alone(g4, ctx, oracle, fmt):
 
 @pytest.mark.parametrize("case", ["t64", "t80_e8", "ff384", "nonfinite", "ref_gates"])
 def test_moe_grouped_by_expert(g4, ctx, oracle, case):
-    """Calls of 64 or more Q4_K tokens run each expert once for all of its (token,
+    """Calls of 40 or more Q4_K tokens run each expert once for all of its (token,
     slot) pairs on the matrix cores (3 x bf16 products, fp32 sums).  The routed
     and the id-taking entry points give the same bits; every output is within the
     bound; a token alone (row kernels) rounds differently but shares the bound.
@@ -648,7 +648,7 @@ def test_moe_routed_dev_calls(g4, ctx, oracle):
 
 @pytest.mark.parametrize("case", ["one_expert", "widest_rows", "ragged_rows", "k8_e256"])
 def test_moe_grouped_edges(g4, ctx, oracle, case):
-    """Edges of the expert-grouped calls (64+ tokens) with the ids given:
+    """Edges of the expert-grouped calls (40+ tokens) with the ids given:
     one_expert: all 256 pairs on one expert (32 passes of eight pairs, the other
     experts idle); widest_rows: 3072 columns (the largest LDS operand set, 150 KB);
     ragged_rows: workgroups left with fewer units than they hold waves for (40
