@@ -312,7 +312,7 @@ class MoeQ4_K(Workload):
         # one token: the down projection and the weighted sum share a launch; 40 or
         # more tokens: a routing launch, then the experts grouped on the matrix cores
         if tokens >= 40:
-            self.dominant_name = ("g4_moe_routed: k_route + k_moe_grp<gate_up> + k_moe_grp<down> (experts grouped "
+            self.dominant_name = ("g4_moe_routed: k_route + k_moe_grp<true> (gate+up) + k_moe_grp<false> (down) (experts grouped "
                                   "on the matrix cores) + k_moe_combine")
         else:
             self.dominant_name = ("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE> (routing + gate_up) + " +
