@@ -717,14 +717,16 @@ def test_moe_dev_out_of_range_ids(g4, ctx, oracle, tokens):
 
 def test_moe_repeated_calls(g4, ctx, oracle):
     """Back-to-back MoE calls on one context with changing token counts: the
-    context's scratch is re-carved per call and nothing leaks from one call to the next."""
+    context's scratch is re-carved per call and nothing leaks from one call to the next.
+    40 tokens run the experts grouped; 33 and 39 take the per-pair launches with
+    pair counts (132, 156) that do not divide the resident workgroups."""
     announce("moe repeated calls")
     E, D, FF, K = 16, 512, 256, 4
     gu = synth.q4_k(48, "gu", E * 2 * FF * D)
     dn = synth.q4_k(48, "dn", E * D * FF)
     wgu = upload(g4, ctx, Q4_K, gu, E * 2 * FF * D)
     wdn = upload(g4, ctx, Q4_K, dn, E * D * FF)
-    for call, T in enumerate([3, 16, 1, 16, 40, 2]):
+    for call, T in enumerate([3, 16, 1, 16, 40, 2, 33, 39]):
         lg = synth.activations(48, "lg%d" % call, T * E).reshape(T, E)
         X = synth.activations(48, "X%d" % call, T * D).reshape(T, D)
         ids, gw = g4.moe_route(ctx, lg, K, True)
