@@ -6,10 +6,9 @@ Default workload: the Q4_0 FFN of one decode token (gate/up W 8192x2048, down W
 y = W_down h -- two launches of libg4hip.so.  Weights are resident in HBM before
 timing starts; each step uses the next of several weight copies whose total
 exceeds twice the 256 MB Infinity Cache, so every step streams from HBM.
-Steps are captured in a HIP graph (one graph = whole passes over the copies,
-at least 8 steps, so a graph replay's own launch cost is spread over several
-steps as in a decode loop) and replayed; the timed region is bracketed by
-device synchronisation.
+The timed steps are captured in one HIP graph (a replay's own launch cost is
+spread over the steps, as in a decode loop) and replayed once; the timed region
+is bracketed by device synchronisation.
 
 Prints one JSON line.  `value` is GB/s of algorithmic bytes (each weight and
 activation byte counted once) per second; `roofline` covers the dominant
@@ -41,7 +40,6 @@ METRIC = "quant matvec GB/s & % of HBM peak (Q8_0/Q4_0/Q4_K); MoE expert tokens/
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 matrix-core peak
 MALL_BYTES = 256 << 20
-GRAPH_MIN_STEPS = 8  # steps per captured graph (whole passes over the copies)
 Q8_0, Q4_0, Q4_K = 8, 2, 12
 
 
@@ -322,8 +320,7 @@ class MoeQ4_K(Workload):
         E, D, FF, K = base["n_experts"], base["dim"], base["ff"], base["k"]
         self.E, self.D, self.FF, self.K = E, D, FF, K
         self.base = base
-        self.wgu = g4.FloatTensorFactory.create(ctx, Q4_K, base["gate_up"], E * 2 * FF * D)
-        self.wdn = g4.FloatTensorFactory.create(ctx, Q4_K, base["down"], E * D * FF)
+        per_expert = (2 * FF * D + D * FF) // 256 * 144
         self.copies = routings
         self.logits, self.X, self.distinct, self.lgh, self.Xh = [], [], [], [], []
         for r in range(routings):  # routing r = the logits/x streams of synth.moe_q4_k(tokens, routing_seed=r)
@@ -338,9 +335,17 @@ class MoeQ4_K(Workload):
         self.ids = torch.zeros((tokens, K), dtype=torch.int32, device="cuda")
         self.gw = torch.zeros((tokens, K), dtype=torch.float32, device="cuda")
         self.Y = torch.empty((tokens, D), dtype=torch.float32, device="cuda")
-        per_expert = (2 * FF * D + D * FF) // 256 * 144
         self.per_expert = per_expert
         mean_distinct = float(np.mean(self.distinct))
+        # expert slab copies: step i reads copy i mod n, with n such that the n - 1
+        # steps between two uses of one copy stream more than twice the Infinity
+        # Cache (all of a step's experts, from HBM, every step)
+        step_experts = mean_distinct * per_expert
+        self.n_slabs = (1 if step_experts >= 2 * MALL_BYTES else
+                        int(math.ceil(2 * MALL_BYTES / step_experts)) + 1)
+        self.slabs = [(g4.FloatTensorFactory.create(ctx, Q4_K, base["gate_up"], E * 2 * FF * D),
+                       g4.FloatTensorFactory.create(ctx, Q4_K, base["down"], E * D * FF))
+                      for _ in range(self.n_slabs)]
         # a step reads every routed expert's gate_up and down once, x and the router
         # logits, and writes Y (the routing outputs are 8 bytes per slot)
         self.step_bytes = int(mean_distinct * per_expert + 4 * tokens * (D + E + D))
@@ -358,12 +363,14 @@ class MoeQ4_K(Workload):
     def step(self, i):
         # routing (inside the gate_up launch), experts and the weighted sum
         r = i % self.copies
-        self.g4.moe_routed_dev(self.ctx, self.wgu, self.wdn, self.X[r], self.T, self.D, self.FF, self.logits[r],
+        wgu, wdn = self.slabs[i % self.n_slabs]
+        self.g4.moe_routed_dev(self.ctx, wgu, wdn, self.X[r], self.T, self.D, self.FF, self.logits[r],
                                self.E, self.K, True, self.ids.data_ptr(), self.gw, self.Y)
 
     def host_step(self, i):
         r = i % self.copies
-        self.g4.moe_routed(self.ctx, self.wgu, self.wdn, self.Xh[r], self.lgh[r], self.K, True, self.D, self.FF)
+        wgu, wdn = self.slabs[i % self.n_slabs]
+        self.g4.moe_routed(self.ctx, wgu, wdn, self.Xh[r], self.lgh[r], self.K, True, self.D, self.FF)
 
     def cpu_setup(self, oracle):
         self.oracle = oracle
@@ -375,7 +382,7 @@ class MoeQ4_K(Workload):
 
     def config(self):
         return {"workload": self.name, "format": "Q4_K", "experts": self.E, "top_k": self.K, "tokens": self.T,
-                "routings": self.copies,
+                "routings": self.copies, "slab_copies": self.n_slabs,
                 "mean_distinct_experts": getattr(self, "mean_used", float(np.mean(self.distinct))),
                 "algorithmic_bytes_per_step": self.step_bytes}
 
@@ -640,17 +647,19 @@ def cpu_baseline(wl: Workload, seconds: float) -> dict:
     return {"value": round(value, 3), "unit": wl.unit, "cores": threads, "kind": "port", "sample": sample}
 
 
-def _time_parts(wl, ctx, stream, torch, copies: int, use_graph: bool, capture) -> list:
+def _time_parts(wl, ctx, stream, torch, steps: int, use_graph: bool, capture) -> list:
     """Average launch time of each separately timed launch of a step: HIP events on
-    the launch stream around back-to-back graph replays of that launch alone,
-    cycling the weight copies (at least 64 launches)."""
+    the launch stream around back-to-back replays of a graph of that launch alone
+    for steps 0 .. steps-1 -- the weight copies and routings the timed steps use,
+    in a graph of the same length as the timed one -- replayed until at least 64
+    launches are timed, after one untimed replay."""
     out = []
-    reps = max(1, math.ceil(64 / copies))
+    reps = max(1, math.ceil(64 / steps))
     for name, nbytes, fn, tkey in wl.parts():
         g = None
         if use_graph:
             try:
-                g = capture(lambda: [fn(i) for i in range(copies)])
+                g = capture(lambda: [fn(i) for i in range(steps)])
             except Exception:
                 g = None
                 torch.cuda.synchronize()
@@ -661,13 +670,13 @@ def _time_parts(wl, ctx, stream, torch, copies: int, use_graph: bool, capture) -
             if g is not None:
                 g.replay()
             else:
-                for i in range(copies):
+                for i in range(steps):
                     fn(i)
         ev1.record(stream)
         torch.cuda.synchronize()
-        us = ev0.elapsed_time(ev1) * 1e3 / (reps * copies)
+        us = ev0.elapsed_time(ev1) * 1e3 / (reps * steps)
         out.append({"kernel": name, "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3),
-                    "launches_timed": reps * copies, "traffic": TRAFFIC_BYTES.get(tkey)})
+                    "launches_timed": reps * steps, "traffic": TRAFFIC_BYTES.get(tkey)})
     return out
 
 
@@ -682,8 +691,6 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool,
         ctx = g4.Context(0)
     wl = make_workload(spec, g4, ctx, torch)
     stream = torch.cuda.Stream()
-    # graphs of part timings replay whole passes over the weight copies
-    copies = wl.copies * max(1, math.ceil(GRAPH_MIN_STEPS / wl.copies))
 
     def capture(fn):
         g = torch.cuda.CUDAGraph()
@@ -717,7 +724,7 @@ def run(spec: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool,
         # timed region: the GPU then runs the timed steps warm, as a decode loop does
         # (the first replays over a large working set, such as the 623 MB of MoE
         # experts, run up to 25% slower)
-        parts = _time_parts(wl, ctx, stream, torch, copies, use_graph, capture)
+        parts = _time_parts(wl, ctx, stream, torch, steps, use_graph, capture)
         ctx.set_stream(stream.cuda_stream)
         torch.cuda.synchronize()
         t0 = time.perf_counter()

@@ -71,8 +71,9 @@ static __device__ __align__(256) unsigned char noalloc_scratch[G4_NOALLOC_SCRATC
 namespace {
 
 constexpr int G4_MAX_DEVICES = 64;
-std::mutex g_noalloc_mu;  // serialises the one-time lookups in g4_open
+std::mutex g_noalloc_mu;  // serialises the one-time per-device set-up in g4_open
 std::atomic<char *> g_noalloc_scratch[G4_MAX_DEVICES];  // device address of noalloc_scratch per ordinal
+bool g_dev_ready[G4_MAX_DEVICES];  // kernel attributes set (under g_noalloc_mu)
 
 thread_local std::string g_last_error;
 
@@ -767,6 +768,20 @@ int g4_open(int ordinal, g4_ctx **out) {
     return hip_fail(e, "hipStreamCreate");
   }
   c->stream = c->own_stream;
+  {
+    // once per device, with the device current: kernel attributes (never set
+    // during a stream capture, since no call sets them)
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (ordinal >= G4_MAX_DEVICES || !g_dev_ready[ordinal]) {
+      e = g4::moe_grp_init_device();
+      if (e != hipSuccess) {
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return hip_fail(e, "hipFuncSetAttribute");
+      }
+      if (ordinal < G4_MAX_DEVICES) g_dev_ready[ordinal] = true;
+    }
+  }
   if (ordinal < G4_MAX_DEVICES) {
     // once per device, with the device current: the address of its copy of the
     // allocation-free entry point's scratch

@@ -252,9 +252,14 @@ struct FmtQ4_0 {
 // (64 weights) uses qs[32g .. 32g+32): low nibbles are sub-block 2g, high
 // nibbles sub-block 2g+1; w = d*sc*q - dmin*m (Q4_KFloatTensor.kt:23-55).
 // Per sub-block: d*sc * sum(x q) - dmin*m * sum(x), each product rounded on its
-// own.  sum(x) runs in the order of sum(x q), so a sub-block whose weights the
-// reference forms as exactly zero (fma(q, d*sc, -dmin*m) = 0, Q4_KFloatTensor.kt:
-// 143-148, i.e. d*sc*q = dmin*m for every q in it) gives exactly 0 here too.
+// own.  sum(x) runs in the order of sum(x q), so sum(x q) = q0 sum(x) exactly
+// when every q of the sub-block is one power of two q0 (scaling by 2^k commutes
+// with every rounding).  A sub-block whose weights the reference forms as
+// exactly zero (fma(q, d*sc, -dmin*m) = 0, Q4_KFloatTensor.kt:143-148) gives
+// exactly 0 here when d*sc = dmin*m = 0, or when its q are all one power of two
+// (such as q = 8 with dmin*m = 8 d*sc) or all 0 with m = 0.  A constant q that is
+// not a power of two (q = 3 with dmin*m = 3 d*sc) leaves a residue of the size of
+// the rounding of sum(x q): a known limit of the factored form.
 struct FmtQ4_K {
   static constexpr int TYPE = T_Q4_K, NDW = 12, NS = 2, RT = 2;
   G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {
@@ -311,7 +316,8 @@ struct FmtQ4_K {
 // 16-byte aligned).  Group g as Q4_K, with the fifth bit of weight l of
 // sub-block s = 2g + h in bit s of qh[l]: q = nibble + 16 bit, w = d*sc*q -
 // dmin*m (Q5_KFloatTensor.kt:23-50).  Per sub-block: d*sc * sum(x q) -
-// dmin*m * sum(x), rounded as for Q4_K (exactly 0 where every weight is).
+// dmin*m * sum(x), rounded as for Q4_K (exactly 0 for the all-zero sub-blocks
+// FmtQ4_K lists: here q0 = 1, 2, 4, 8 or 16).
 struct FmtQ5_K {
   static constexpr int TYPE = T_Q5_K, NDW = 20, NS = 2, RT = 2;
   G4_DEV static void load(const uint8_t *W, int64_t e, uint32_t (&D)[NDW]) {

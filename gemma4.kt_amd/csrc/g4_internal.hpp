@@ -123,6 +123,9 @@ struct MoeGrpArgs {
   int64_t y_stride;
 };
 bool moe_grp_ok(int type, const MoeGrpArgs &a);
+// Grants the grouped kernels their largest dynamic LDS size on the current
+// device; called once per device before any launch (g4_open).
+hipError_t moe_grp_init_device();
 hipError_t launch_moe_grp(int type, bool gate_up, const MoeGrpArgs &a, const DevInfo &dev, hipStream_t stream);
 
 // Plain matvec of rows of 65..256 chunks (g4_wide.hip): the columns split over

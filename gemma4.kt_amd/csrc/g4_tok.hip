@@ -10,10 +10,13 @@
 //     16(q - 8) in -128..112 is an exact bf16, and the sub-block's two fp32
 //     coefficients are applied after the products, as
 //     (d*sc/16) * sum(16(q - 8) x) + (8 d*sc - dmin*m) * sum(x).  8 d*sc is
-//     exact, so a sub-block whose weights are all exactly zero (q = 8 and
-//     8 d*sc = dmin*m) contributes exactly 0, as in the reference, whose
-//     fma(q, d*sc, -dmin*m) forms each weight first (Q4_KFloatTensor.kt:143-148);
-//     and the rounding of the sums scales with |q - 8| rather than with q;
+//     exact, so a sub-block of weights that are all exactly zero contributes
+//     exactly 0, as in the reference, whose fma(q, d*sc, -dmin*m) forms each
+//     weight first (Q4_KFloatTensor.kt:143-148), when q = 8 and 8 d*sc =
+//     dmin*m, or d*sc = dmin*m = 0.  Other all-zero sub-blocks (a constant
+//     q0 != 8 with dmin*m = q0 d*sc) leave a residue of the size of the
+//     rounding of the two sums: a known limit.  The rounding of the sums scales
+//     with |q - 8| rather than with q;
 //   * activations: an fp32 x has 24 significant bits and splits exactly into
 //     x1 + x2 + x3, three round-to-nearest bf16 parts of 8 bits each, so three
 //     MFMAs give sum(q x) with exact products and fp32 accumulation.
@@ -773,20 +776,23 @@ bool moe_grp_ok(int type, const MoeGrpArgs &a) {
   return a.S >= 1 && a.S <= MG_MAX_S && a.rows >= 1 && a.x_div >= 1 && a.n_experts >= 1;
 }
 
+hipError_t moe_grp_init_device() {
+  // the largest LDS operand set (MG_MAX_DIM1 columns), granted once per device
+  const int lds = (int)mg_lds_bytes(MG_MAX_DIM1);
+  hipError_t e = hipFuncSetAttribute((const void *)k_moe_grp<true>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (e != hipSuccess) return e;
+  return hipFuncSetAttribute((const void *)k_moe_grp<false>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+}
+
 hipError_t launch_moe_grp(int type, bool gate_up, const MoeGrpArgs &a, const DevInfo &dev, hipStream_t s) {
   (void)dev;
   if (!moe_grp_ok(type, a)) return hipErrorNotSupported;
   const int ur = gate_up ? 16 : 32;
   const int units = (a.rows + ur - 1) / ur;
   const dim3 grid((unsigned)((units + MG_UPW * MG_WPB - 1) / (MG_UPW * MG_WPB)), (unsigned)a.n_experts + 1);
+  // up to mg_lds_bytes(MG_MAX_DIM1) of dynamic LDS: granted by moe_grp_init_device
+  // when the context opened (a host-side attribute, never set during a capture)
   const size_t lds = mg_lds_bytes(a.dim1);
-  const void *k = gate_up ? (const void *)k_moe_grp<true> : (const void *)k_moe_grp<false>;
-  // more than 64 KB of dynamic LDS is granted per kernel (a host-side attribute of
-  // the current device, not a stream operation)
-  if (lds > 65536) {
-    const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-  }
   if (gate_up)
     hipLaunchKernelGGL(k_moe_grp<true>, grid, dim3(MG_WPB * 64), lds, s, a);
   else

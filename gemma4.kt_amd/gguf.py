@@ -14,6 +14,13 @@ to `FloatTensorFactory.create`, which uploads the raw GGUF blocks once to device
 memory (g4_upload; no repacking).  Formats the device path does not implement
 raise UnsupportedOperationException there; a host keeps its CPU tensor for them.
 
+Scope: this module exists to reach the tensor table (infos, alignment, data
+offset) that the upload hook needs.  GGUF stores the tensor infos after the
+metadata, and each metadata value's length depends on its type, so the table is
+walked and kept as the reference keeps it; nothing here interprets metadata
+beyond the alignment, and the model loader above loadQuantized (hyperparameters,
+tokenizer) is not built.
+
 Byte order is little-endian throughout (ChannelReader.kt:10).  Values are read
 as the reference reads them: UINT8/UINT16/UINT32/UINT64 as the signed type of
 the same width (readByte/readShort/readInt/readLong).

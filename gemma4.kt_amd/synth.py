@@ -289,13 +289,26 @@ def q8_0_lm_head_block(seed: int = SEED_Q8_0_LM_HEAD, vocab: int = 262144, dim: 
     return d
 
 
+_MOE_SLABS = {}
+
+
 def moe_q4_k(tokens: int, seed: int = SEED_MOE_Q4_K, n_experts: int = 128, dim: int = 2048,
              ff: int = 1408, k: int = 8, routing_seed: int = 0) -> dict:
     """128 Q4_K experts (gate_up [E x 2ff x dim], down [E x dim x ff]), router
     logits ~ N(0,1) [tokens x E], X ~ N(0,1) [tokens x dim], top-k routing.
-    routing_seed selects one of many independent routings/activations."""
-    return dict(gate_up=q4_k(seed, "gate_up", n_experts * 2 * ff * dim),
-                down=q4_k(seed, "down", n_experts * dim * ff),
+    routing_seed selects one of many independent routings/activations.  The
+    expert slabs do not depend on the token count: they are generated once per
+    shape and shared by later calls (read-only arrays)."""
+    key = (seed, n_experts, dim, ff)
+    if key not in _MOE_SLABS:
+        gu = q4_k(seed, "gate_up", n_experts * 2 * ff * dim)
+        dn = q4_k(seed, "down", n_experts * dim * ff)
+        gu.flags.writeable = False
+        dn.flags.writeable = False
+        _MOE_SLABS.clear()
+        _MOE_SLABS[key] = (gu, dn)
+    gu, dn = _MOE_SLABS[key]
+    return dict(gate_up=gu, down=dn,
                 logits=activations(seed, "router%d.%d" % (tokens, routing_seed), tokens * n_experts)
                 .reshape(tokens, n_experts),
                 x=activations(seed, "x%d.%d" % (tokens, routing_seed), tokens * dim).reshape(tokens, dim),

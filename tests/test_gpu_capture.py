@@ -32,6 +32,21 @@ def moe_weights(g4, ctx):
     wdn.free()
 
 
+@pytest.fixture(scope="module")
+def wide_moe_weights(g4, ctx):
+    """The configured expert shape (dim 2048, ff 1408): its grouped launches need
+    about 98 KB (gate+up) and 67 KB (down) of LDS, more than the 64 KB a kernel
+    gets without its attribute."""
+    E, dim, ff = 8, 2048, 1408
+    gu = synth.q4_k(42, "gu", E * 2 * ff * dim)
+    dn = synth.q4_k(42, "dn", E * dim * ff)
+    wgu = g4.FloatTensorFactory.create(ctx, Q4_K, gu, E * 2 * ff * dim)
+    wdn = g4.FloatTensorFactory.create(ctx, Q4_K, dn, E * dim * ff)
+    yield dict(E=E, dim=dim, ff=ff, k=4, wgu=wgu, wdn=wdn)
+    wgu.free()
+    wdn.free()
+
+
 def _io(mw, T, seed):
     X = torch.from_numpy(synth.activations(seed, "x", T * mw["dim"]).reshape(T, mw["dim"])).cuda()
     lg = torch.from_numpy(synth.activations(seed, "lg", T * mw["E"]).reshape(T, mw["E"])).cuda()
@@ -92,14 +107,16 @@ def test_replays_survive_a_later_scratch_regrowth(g4, moe_weights):
         c.close()
 
 
-def test_grouped_moe_replays(g4, moe_weights):
+@pytest.mark.parametrize("shape", ["dim512", "dim2048_ff1408"])
+def test_grouped_moe_replays(g4, request, shape):
     """A call of 96 tokens runs the experts grouped by expert: a routing launch, two
-    grouped launches (their LDS size granted per launch by a host-side kernel
-    attribute, legal under capture) and the combine.  Captured once and replayed
-    three times, with eager grouped and per-pair calls between the replays: every
-    replay gives the eager bits."""
-    announce("capture: grouped MoE replays")
-    mw = moe_weights
+    grouped launches and the combine.  At dim 2048 / ff 1408 the grouped kernels
+    use more than 64 KB of LDS (granted once per device when the context opens,
+    never inside a capture).  Captured once and replayed three times, with eager
+    grouped and per-pair calls between the replays: every replay gives the eager
+    bits."""
+    announce("capture: grouped MoE replays %s" % shape)
+    mw = request.getfixturevalue("moe_weights" if shape == "dim512" else "wide_moe_weights")
     c = g4.Context(0)
     stream = torch.cuda.Stream()
     try:

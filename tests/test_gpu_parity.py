@@ -390,10 +390,11 @@ def test_q4_k_batched(g4, ctx, oracle, m):
     R, D = c["dim0"], c["dim1"]
     w = upload(g4, ctx, Q4_K, c["w"], R * D)
     Y = w.matmul_batch(c["x"], R, D)
-    rows = np.arange(R) if m <= 8 else np.random.default_rng(m).choice(R, 512, replace=False)
+    # every row of every token (a tile or row-range indexing error that only the
+    # full grid reaches shows here)
     for i in range(m):
         ex, ab = oracle.matmul_exact(Q4_K, c["w"], c["x"][i], R, D)
-        assert_dots(Y[i][rows], ex[rows], ab[rows], "batched m=%d row %d" % (m, i))
+        assert_dots(Y[i], ex, ab, "batched m=%d token %d" % (m, i))
 
 
 # matrix-core multi-token kernel (M >= 3): partial row and token tiles, several
@@ -467,13 +468,27 @@ def test_moe_route_exact(g4, ctx, oracle, tokens, renorm):
     assert same_bits(w, rw)
 
 
-@pytest.mark.parametrize("tokens", [1, 16])
+_MOE_SLABS = {}
+
+
+def moe_slabs(g4, ctx, c):
+    """The 623 MB of expert slabs of the MoE workload, generated and uploaded once
+    for every token count (they do not depend on it)."""
+    if "w" not in _MOE_SLABS:
+        E, D, FF = c["n_experts"], c["dim"], c["ff"]
+        _MOE_SLABS["w"] = (upload(g4, ctx, Q4_K, c["gate_up"], E * 2 * FF * D),
+                           upload(g4, ctx, Q4_K, c["down"], E * D * FF))
+    return _MOE_SLABS["w"]
+
+
+# the configured workload (128 experts, top-8, dim 2048, ff 1408): one token and
+# 16 tokens take the per-pair launches, 40 and 128 the expert-grouped ones
+@pytest.mark.parametrize("tokens", [1, 16, 40, 128])
 def test_moe_q4_k(g4, ctx, oracle, tokens):
     announce("workload moe q4_k T=%d" % tokens)
     c = synth.moe_q4_k(tokens)
     E, D, FF, K = c["n_experts"], c["dim"], c["ff"], c["k"]
-    wgu = upload(g4, ctx, Q4_K, c["gate_up"], E * 2 * FF * D)
-    wdn = upload(g4, ctx, Q4_K, c["down"], E * D * FF)
+    wgu, wdn = moe_slabs(g4, ctx, c)
     ids, gw = g4.moe_route(ctx, c["logits"], K, True)
     rids, rw = oracle.route(c["logits"], K, True)
     assert np.array_equal(ids, rids) and same_bits(gw, rw)
@@ -573,8 +588,8 @@ def test_moe_grouped_by_expert(g4, ctx, oracle, case):
     slot) pairs on the matrix cores (3 x bf16 products, fp32 sums).  The routed
     and the id-taking entry points give the same bits; every output is within the
     bound; a token alone (row kernels) rounds differently but shares the bound.
-    t80_e8: ten pairs per expert on average, so experts take up to four passes of
-    four pairs; ff384: down rows of 384 columns, every second one starting half
+    t80_e8: ten pairs per expert on average, so experts take two or more passes
+    of eight pairs; ff384: down rows of 384 columns, every second one starting half
     way into a super-block; nonfinite: +inf, NaN and -inf activations reach only
     their own tokens; ref_gates: un-renormalised gates times a per-expert down
     scale (Llama.kt:300-337)."""
