@@ -131,10 +131,11 @@ constexpr int TOK_GPW = 2;
 // by a fixed stride per row tile, and the wave's two groups lie in one
 // super-block, whose head is loaded once and whose four sub-blocks' scales
 // take wave-uniform byte positions.
-template <int TT, int WPB, bool AL>
+template <int TT, int WPB, bool AL, bool HALF>
 __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   constexpr int GPW = TOK_GPW, NH = AL ? 1 : GPW;
   static_assert(TT * GPW <= TOK_SLOTS && WPB >= TT && WPB % TT == 0, "tile shape");
+  static_assert(!HALF || TT == 1, "HALF: one token tile of at most 8 tokens");
   // LDS: first each wave's x slice (16 tokens x 128 columns, rows padded to
   // XROW floats so the reads below are conflict-free), then, after a barrier,
   // the cross-wave partial tiles
@@ -221,7 +222,9 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   // x slice: 16 tokens x the wave's 128 columns, read so that adjacent lanes
   // take adjacent 16-byte pieces (each instruction two tokens' 512 contiguous
   // bytes: lane l takes piece l % 32 of token 2q + l / 32) and staged in LDS;
-  // columns of groups past the slice come from group 0 (in bounds, never used)
+  // columns of groups past the slice come from group 0 (in bounds, never used);
+  // HALF (at most 8 tokens): tokens 8..15 are not read but staged as zeros, so
+  // the wave issues half the x loads
   u32x4a4 xg[TT][8];
 #pragma unroll
   for (int ti = 0; ti < TT; ++ti)
@@ -229,7 +232,7 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
     for (int q = 0; q < 8; ++q) {
       const int tok = (tt0 + ti) * 16 + 2 * q + (lane >> 5), c = lane & 31, gi = c >> 4;
       const float *p = a.x + (int64_t)(tok < a.M ? tok : 0) * a.x_stride + (int64_t)(gi < ng ? g0 + gi : 0) * 64 + 4 * (c & 15);
-      xg[ti][q] = *(const u32x4a4 *)p;
+      xg[ti][q] = (HALF && q >= 4) ? u32x4a4{0u, 0u, 0u, 0u} : *(const u32x4a4 *)p;
     }
   u32x2a4 QA[GPW], QB[GPW];
   u32x4 HA[NH], HB[NH];
@@ -513,10 +516,16 @@ hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_
   const dim3 grid((unsigned)sh.gx, (unsigned)sh.splits, (unsigned)sh.tgroups);
   // whole super-blocks per row and an even number of groups: every wave's two
   // groups lie in one super-block
-  if ((a.base % 256) == 0 && (a.row_stride % 256) == 0 && (a.dim1 % 128) == 0)
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
+  // at most 8 tokens: the x loads of tokens 8..15 are left out
+  const bool al = (a.base % 256) == 0 && (a.row_stride % 256) == 0 && (a.dim1 % 128) == 0, half = a.M <= 8;
+  if (al && half)
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
+  else if (al)
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
+  else if (half)
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
   else
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
   if (sh.splits == 1) return hipGetLastError();
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
