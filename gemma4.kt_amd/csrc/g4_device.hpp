@@ -630,19 +630,19 @@ G4_DEV void am_wave(float &v, int &i) {
 // the last double bit can differ from StrictMath.tanh; the JVM's Math.tanh may
 // also run an intrinsic of its own.  Bit parity with the reference's tanh is
 // therefore not claimed: the result is within 2 ulps of tanh.
+// The two middle cases share one expm1 and one division, their operands chosen
+// per lane (the same operations on each lane as the branches, without running
+// both when the lanes of a wave fall on different sides of |x| = 1).
 G4_DEV double tanh_fdlibm(double x) {
   const double ax = fabs(x);
-  if (x != x) return x + x;
-  if (ax < 0x1p-55) return x * (1.0 + x);
-  double z = 1.0;
-  if (ax < 1.0) {
-    const double t = expm1(-2.0 * ax);
-    z = -t / (t + 2.0);
-  } else if (ax < 22.0) {
-    const double t = expm1(2.0 * ax);
-    z = 1.0 - 2.0 / (t + 2.0);
-  }
-  return __builtin_signbit(x) ? -z : z;
+  const bool small = ax < 1.0;
+  const double t = expm1(small ? -2.0 * ax : 2.0 * ax);
+  const double qt = (small ? -t : 2.0) / (t + 2.0);  // -t / (t + 2), or 2 / (t + 2)
+  double z = small ? qt : 1.0 - qt;
+  z = ax < 22.0 ? z : 1.0;
+  z = __builtin_signbit(x) ? -z : z;
+  z = ax < 0x1p-55 ? x * (1.0 + x) : z;
+  return x != x ? x + x : z;
 }
 
 // Llama.kt:23-25 gelu, evaluated in double like the reference.
