@@ -59,6 +59,35 @@ G4_DEV float bf2f(uint32_t h16) { return __uint_as_float((h16 & 0xFFFFu) << 16);
 G4_DEV float sbyte(uint32_t v, int b) { return (float)(int8_t)(v >> (8 * b)); }  // v_cvt_f32_i32_sdwa sext
 G4_DEV float ubyte(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }  // v_cvt_f32_ubyte{b}
 
+// f16 bit patterns below 0x0400 are the subnormals k * 2^-24: integers k < 1024
+// masked into the two 16-bit halves of a dword are two exact f16 values, and
+// v_fma_mix_f32 converts either half inside its fma (op_sel), so one AND
+// unpacks two weights and the product with x costs one instruction.  Each
+// product and sum is the one with k, scaled by 2^-24 exactly: roundings
+// commute with power-of-two scaling while the values stay normal (|x| above
+// 2^-102 or so), and the kernels' scales carry the 2^24 back.
+G4_DEV float f16lo(uint32_t m) { return (float)__builtin_bit_cast(_Float16, (uint16_t)m); }
+G4_DEV float f16hi(uint32_t m) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(m >> 16)); }
+
+// lo + sum over the four bytes b of q, in byte order, of xl[b] * 2^-24 * (the
+// low nibble of byte b), and hi + the same of xh[b] * 2^-24 * 16 * (its high
+// nibble).  Bytes 0 and 2 come from q, bytes 1 and 3 from q >> 8.  The two
+// chains alternate: a v_fma_mix_f32 that reads the result of the one before
+// it waits a cycle.
+G4_DEV void nib4_fma2(uint32_t q, const float *xl, const float *xh, float &lo, float &hi) {
+  const uint32_t c = q >> 8;
+  const uint32_t al = opaque(q & 0x000F000Fu), ah = opaque(q & 0x00F000F0u);
+  const uint32_t cl = opaque(c & 0x000F000Fu), ch = opaque(c & 0x00F000F0u);
+  lo = __builtin_fmaf(f16lo(al), xl[0], lo);
+  hi = __builtin_fmaf(f16lo(ah), xh[0], hi);
+  lo = __builtin_fmaf(f16lo(cl), xl[1], lo);
+  hi = __builtin_fmaf(f16lo(ch), xh[1], hi);
+  lo = __builtin_fmaf(f16hi(al), xl[2], lo);
+  hi = __builtin_fmaf(f16hi(ah), xh[2], hi);
+  lo = __builtin_fmaf(f16hi(cl), xl[3], lo);
+  hi = __builtin_fmaf(f16hi(ch), xh[3], hi);
+}
+
 G4_DEV uint32_t rd_u8(const uint8_t *p) { return *p; }
 G4_DEV uint32_t rd_u16(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
 
@@ -220,19 +249,13 @@ struct FmtQ4_0 {
       s[k] = t;
     }
   }
-  // sl / sh: the sums of x over the block's low / high 16 elements
+  // sl / sh: the sums of x over the block's low / high 16 elements; the result
+  // is scaled by 2^-24 (nib4_fma2), as are -8 and -128
   G4_DEV static float block(const uint32_t (&Q)[4], const float *x, float sl, float sh) {
     float lo = 0.f, hi = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t l = opaque(Q[i] & 0x0F0F0F0Fu), h = opaque(Q[i] & 0xF0F0F0F0u);
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        lo = __builtin_fmaf(x[4 * i + b], ubyte(l, b), lo);
-        hi = __builtin_fmaf(x[16 + 4 * i + b], ubyte(h, b), hi);
-      }
-    }
-    return __builtin_fmaf(__builtin_fmaf(-128.f, sh, hi), 0.0625f, __builtin_fmaf(-8.f, sl, lo));
+    for (int i = 0; i < 4; ++i) nib4_fma2(Q[i], x + 4 * i, x + 16 + 4 * i, lo, hi);
+    return __builtin_fmaf(__builtin_fmaf(-0x1p-17f, sh, hi), 0.0625f, __builtin_fmaf(-0x1p-21f, sl, lo));
   }
   G4_DEV static float dot(const uint32_t (&D)[NDW], const float *x, const float *s, int64_t e) {
     (void)e;
@@ -244,7 +267,7 @@ struct FmtQ4_0 {
     }
     float t0 = block(Q0, x, s[0], s[1]);
     float t1 = block(Q1, x + 32, s[2], s[3]);
-    return __builtin_fmaf(h2f(D[0] & 0xFFFFu), t0, h2f(D[4] >> 16) * t1);
+    return __builtin_fmaf(h2f(D[0] & 0xFFFFu) * 0x1p24f, t0, (h2f(D[4] >> 16) * 0x1p24f) * t1);
   }
 };
 
@@ -278,16 +301,9 @@ struct FmtQ4_K {
     s[0] = s0; s[1] = s1;
   }
   G4_DEV static float dot(const uint32_t (&D)[NDW], const float *x, const float *s, int64_t e) {
-    float lo = 0.f, hi = 0.f;
+    float lo = 0.f, hi = 0.f;  // scaled by 2^-24 (nib4_fma2); d carries 2^24
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t l = opaque(D[i] & 0x0F0F0F0Fu), h = opaque(D[i] & 0xF0F0F0F0u);
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        lo = __builtin_fmaf(x[4 * i + b], ubyte(l, b), lo);
-        hi = __builtin_fmaf(x[32 + 4 * i + b], ubyte(h, b), hi);
-      }
-    }
+    for (int i = 0; i < 8; ++i) nib4_fma2(D[i], x + 4 * i, x + 32 + 4 * i, lo, hi);
     // getScaleMinK4 (Q4_KFloatTensor.kt:70-84) for sub-blocks 2g and 2g+1: both
     // live in bytes 2(g&1), 2(g&1)+1 of the three scale dwords.
     const int g = (int)((e >> 6) & 3);
@@ -301,7 +317,7 @@ struct FmtQ4_K {
       scp = (w & 0x0F0Fu) | ((y >> 2) & 0x3030u);
       mp = ((w >> 4) & 0x0F0Fu) | ((z >> 2) & 0x3030u);
     }
-    const float d = h2f(D[8] & 0xFFFFu), dmin = h2f(D[8] >> 16);
+    const float d = h2f(D[8] & 0xFFFFu) * 0x1p24f, dmin = h2f(D[8] >> 16);
     const float d1 = d * ubyte(scp, 0), d2 = d * ubyte(scp, 1) * 0.0625f;
     const float m1 = dmin * ubyte(mp, 0), m2 = dmin * ubyte(mp, 1);
     return k_subblocks(d1, lo, m1, s[0], d2, hi, m2, s[1]);
