@@ -397,6 +397,61 @@ def test_q4_k_batched(g4, ctx, oracle, m):
         assert_dots(Y[i], ex, ab, "batched m=%d token %d" % (m, i))
 
 
+def _integer_blocks(t, n, seed):
+    """Blocks of type t whose weights are all small integers: unit d (and dmin),
+    scales and mins in 0..3 (Q6_K: -3..3), every quant field random.  With integer
+    x in -3..3 every product and every partial sum of a dot is an exact fp32
+    integer (below 2^24 for the sizes used here)."""
+    rng = np.random.default_rng(seed)
+    one = synth.fp16_bits(np.array([1.0])).view(np.uint8)
+    if t == Q8_0:
+        raw = synth.q8_0(seed, "int", n).reshape(-1, 34)
+        raw[:, 0:2] = one
+    elif t == Q4_0:
+        raw = synth.q4_0(seed, "int", n).reshape(-1, 18)
+        raw[:, 0:2] = one
+    elif t in (Q4_K, Q5_K):
+        raw = (synth.q4_k if t == Q4_K else synth.q5_k)(seed, "int", n).reshape(n // 256, -1)
+        raw[:, 0:2] = one
+        raw[:, 2:4] = one
+        raw[:, 4:16] = synth.pack_q4k_scales(rng.integers(0, 4, (n // 256, 8)), rng.integers(0, 4, (n // 256, 8)))
+    else:
+        raw = synth.q6_k(seed, "int", n).reshape(-1, 210)
+        raw[:, 192:208] = rng.integers(-3, 4, (n // 256, 16)).astype(np.int8).view(np.uint8)
+        raw[:, 208:210] = one
+    return raw.reshape(-1)
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q5_K, Q6_K])
+@pytest.mark.parametrize("rows,cols", [(64, 2048), (96, 1408), (8, 16384), (40, 512)])
+def test_integer_dots_exact(g4, ctx, oracle, t, rows, cols):
+    """Integer weights (every quant value at every position, scales and mins
+    unpacked) against integer x: every kernel must return the exact dot, so a
+    weight unpacked, placed or scaled wrongly shows as an integer error, not as
+    rounding.  One column pass (2048), x read at use (1408 = 22 chunks), several
+    passes and the wide rows (16384), 16-lane rows (512); Q4_K also through the
+    matrix-core kernel (M = 8 and 33)."""
+    announce("integer dots type %d %dx%d" % (t, rows, cols))
+    n = rows * cols
+    raw = _integer_blocks(t, n, 81 + t)
+    W = oracle.dequant(t, raw, 0, n).reshape(rows, cols).astype(np.float64)
+    assert np.all(W == np.round(W)) and np.max(np.abs(W)) < 512
+    rng = np.random.default_rng(82 + cols)
+    X = rng.integers(-3, 4, (33, cols)).astype(np.float32)
+    w = upload(g4, ctx, t, raw, n)
+    y = np.empty(rows, np.float32)
+    w.matmul(X[0], y, rows, cols)
+    ex = W @ X[0].astype(np.float64)
+    assert np.array_equal(y.astype(np.float64), ex), "matvec: %r vs %r" % (y[y != ex][:4], ex[y != ex][:4])
+    for m in ((8, 33) if t == Q4_K else (3,)):
+        Y = w.matmul_batch(X[:m], rows, cols)
+        EX = X[:m].astype(np.float64) @ W.T
+        bad = np.argwhere(Y.astype(np.float64) != EX)
+        assert bad.size == 0, "batched M=%d: %d wrong, first %r: %r vs %r" % (
+            m, len(bad), tuple(bad[0]), Y[tuple(bad[0])], EX[tuple(bad[0])])
+    w.free()
+
+
 # matrix-core multi-token kernel (M >= 3): partial row and token tiles, several
 # column splits (summed by the reduce launch: 4224 and 4096 columns), rows that
 # start mid super-block (1408 = 5.5 super-blocks), a row offset, a single
