@@ -268,9 +268,10 @@ class BatchedQ4_K(Workload):
         self.c, self.m = c, m
         # one or two tokens: the row-stream kernel (one segment per token); three or
         # more: the matrix-core kernel (one column split up to 2048 columns, more
-        # splits summed by k_tok_reduce)
+        # splits summed by k_tok_reduce), its HALF form (token rows 8..15 not
+        # loaded) up to eight tokens
         self.dominant_name = ("k_rows<FmtQ4_K, 32, EPI_STORE>" if m <= 2 else
-                              "k_tok_q4k<1, 16, true> (bf16x3 MFMA 16x16x32)")
+                              "k_tok_q4k<1, 16, true, %s> (bf16x3 MFMA 16x16x32)" % ("true" if m <= 8 else "false"))
         self.name = "q4_k_batched_8192x2048_m%d" % m
         R, D = c["dim0"], c["dim1"]
         self.R, self.D = R, D
