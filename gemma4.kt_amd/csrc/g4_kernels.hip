@@ -825,6 +825,121 @@ __global__ __launch_bounds__(64 * WPB) void k_moe_down(RowsArgs a, const float *
   }
 }
 
+// The same in the 8-wave shape for rows of 17..24 chunks (the MoE's 1408-column
+// down rows are 22): 8 lanes x 3 chunks per row, so 22 of 24 lanes work against
+// 22 of 32 with one chunk per lane, one row step of 8 rows per wave and slot.
+// Each chunk's x is read from LDS right before its dot and the Q-format block
+// sums of x are formed once per (slot, chunk), as k_rows' x-read-at-use form
+// does: every dot has the bits of the per-pair XL launch, and the k row values
+// are summed in slot order as k_moe_combine does.
+template <class F>
+__global__ __launch_bounds__(512) void k_moe_down_xl(RowsArgs a, const float *gw, int32_t K) {
+  constexpr int NT = 512, LPR = 8, CPL = 3, NCH = LPR * CPL, RPW = 64 / LPR, TR = RPW, NDW = F::NDW;
+  constexpr int NSX = F::NS > 0 ? F::NS : 1;
+  constexpr int XS = NCH * 16;                    // 16-byte x segments of one slot
+  constexpr int XSEG = MOE_DOWN_MAX_K * XS / NT;  // staged by each thread
+  static_assert(XSEG * NT == MOE_DOWN_MAX_K * XS, "x staging");
+  static_assert(MOE_DOWN_MAX_K * NCH <= NT, "one thread per (slot, chunk) for the block sums");
+  // chunk ch's segment i at slot ch * 17 + i (a chunk's 16 reads share one
+  // address; the 8 chunks one LDS cycle serves land in different bank groups)
+  __shared__ u32x4 xl[MOE_DOWN_MAX_K][NCH * 17];
+  __shared__ float xsl[MOE_DOWN_MAX_K][NCH][NSX];
+  __shared__ float cb[MOE_DOWN_MAX_K][TR];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gi = lane / LPR, q = lane % LPR;
+  const int tok = blockIdx.y;
+  const int C = a.dim1 >> 6;
+  const int row0 = blockIdx.x * TR;
+
+  // every slot's x segments, masked past K and past the row (loads never branch)
+  u32x4a4 xr[XSEG];
+#pragma unroll
+  for (int u = 0; u < XSEG; ++u) {
+    const int g = u * NT + tid, j = g / XS, c = (g % XS) >> 4;
+    const bool in = (j < K) & (c < C);
+    const float *xp = a.x + (int64_t)(tok * K + (in ? j : 0)) * a.x_stride + (int64_t)(in ? c : 0) * 64;
+    xr[u] = ((const u32x4a4 *)xp)[g & 15];
+  }
+  float w_slot[MOE_DOWN_MAX_K];
+  if (tid < TR) {
+#pragma unroll
+    for (int j = 0; j < MOE_DOWN_MAX_K; ++j) w_slot[j] = gw[tok * K + (j < K ? j : 0)];
+  }
+  // wave wid's slot: its row step's weights (a slot past K loads the tensor's
+  // first chunk, masked)
+  uint32_t D[CPL][NDW];
+  bool ok[CPL];
+  int64_t E[CPL];
+  {
+    const int j = wid;
+    const int expert = a.ids[tok * K + (j < K ? j : 0)];
+    const bool bad = (j >= K) | (expert < 0) | (expert >= a.expert_count);
+    const int64_t ebase = bad ? 0 : (int64_t)expert * a.expert_stride;
+    const int lr = row0 + gi;
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+      const int c = u * LPR + q;
+      ok[u] = !bad && c < C && lr < a.rows;
+      E[u] = a.base0 + ebase + (int64_t)lr * a.row_stride + (int64_t)c * 64;
+      F::load(a.W0, ok[u] ? E[u] : 0, D[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < XSEG; ++u) {
+    const int g = u * NT + tid, j = g / XS, c = (g % XS) >> 4;
+    const uint32_t m = opaque(((j < K) & (c < C)) ? ~0u : 0u);
+    xl[j][c * 17 + (g & 15)] = u32x4{xr[u].x & m, xr[u].y & m, xr[u].z & m, xr[u].w & m};
+  }
+  __syncthreads();
+  auto read_x = [&](int j, int ch, float (&xu)[64]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const u32x4 t = xl[j][ch * 17 + i];
+      xu[4 * i] = __uint_as_float(t.x);
+      xu[4 * i + 1] = __uint_as_float(t.y);
+      xu[4 * i + 2] = __uint_as_float(t.z);
+      xu[4 * i + 3] = __uint_as_float(t.w);
+    }
+  };
+  if constexpr (F::NS > 0) {
+    if (tid < MOE_DOWN_MAX_K * NCH) {
+      const int j = tid / NCH, ch = tid % NCH;
+      float xu[64], su[NSX];
+      read_x(j, ch, xu);
+      F::sums(xu, su);
+#pragma unroll
+      for (int i = 0; i < NSX; ++i) xsl[j][ch][i] = su[i];
+    }
+    __syncthreads();
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (wid < K) {
+    float acc = 0.f;  // the per-pair launch's accumulation, bit for bit
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+      float xu[64], su[NSX];
+      const int ch = (int)opaque((uint32_t)(u * LPR + q));
+      read_x(wid, ch, xu);
+#pragma unroll
+      for (int i = 0; i < NSX; ++i) su[i] = xsl[wid][ch][i];
+      float r = F::dot(D[u], xu, su, E[u]);
+      // one chunk's x in VGPRs at a time
+      asm volatile("" : "+v"(r)::"memory");
+      acc += ok[u] ? r : 0.f;
+    }
+    float v[1] = {acc};
+    const float r = reduce_transpose<1, LPR>(v, lane);
+    if (q == 0) cb[wid][gi] = r;
+  }
+  __syncthreads();
+  if (tid < TR && row0 + tid < a.rows) {
+    float out = 0.f;
+    for (int j = 0; j < K; ++j) out = rounded(w_slot[j] * cb[j][tid]) + out;
+    a.y[(int64_t)tok * a.y_stride + row0 + tid] = out;
+  }
+}
+
 // Y[t*dim + r] = sum_j w[t,j] * ys[(t*K + j)*dim + r] in j order, a*d + out like
 // saxpyInPlace (MutableFloatTensor.kt:61-66).
 __global__ void k_moe_combine(const float *ys, const float *w, int32_t T, int32_t K, int32_t dim, float *Y) {
@@ -1273,6 +1388,14 @@ static hipError_t launch_moe_down_cfg(const RowsArgs &a, const float *gw, int32_
   constexpr int TR8 = 2 * F::RT * (64 / LPR), TR4 = F::RT * (64 / LPR);
   const int64_t n8 = (a.rows + TR8 - 1) / TR8, n4 = (a.rows + TR4 - 1) / TR4;
   if (n8 * T <= (int64_t)dev.cu_count) {
+    // rows of 17..24 chunks: 8 lanes x 3 chunks (the same 8 rows per workgroup
+    // when LPR is 32), for the formats whose three chunk buffers fit the VGPRs
+    if constexpr (F::NDW <= 20 && LPR == 32 && TR8 == 8) {
+      if (a.dim1 <= 24 * 64) {
+        hipLaunchKernelGGL(k_moe_down_xl<F>, dim3((unsigned)n8, T), dim3(512), 0, s, a, gw, K);
+        return hipGetLastError();
+      }
+    }
     hipLaunchKernelGGL((k_moe_down<F, LPR, 8>), dim3((unsigned)n8, T), dim3(512), 0, s, a, gw, K);
     return hipGetLastError();
   }
