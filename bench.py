@@ -312,15 +312,16 @@ class MoeQ4_K(Workload):
         import synth
         self.T = tokens
         self.name = "moe_q4_k_128x(2816x2048+2048x1408)_top8_t%d" % tokens
-        # one token: the down projection and the weighted sum share a launch; 40 or
+        # up to 39 tokens: the down projection and the weighted sum share a launch
+        # (one row step per wave for one token, looped row steps for more); 40 or
         # more tokens: a routing launch, then the experts grouped on the matrix cores
         if tokens >= 40:
             self.dominant_name = ("g4_moe_routed: k_route + k_moe_grp<true> (gate+up) + k_moe_grp<false> (down) (experts grouped "
                                   "on the matrix cores) + k_moe_combine")
         else:
             self.dominant_name = ("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE> (routing + gate_up) + " +
-                                  ("k_moe_down<FmtQ4_K, 32, 8> (down + weighted sum)" if tokens == 1 else
-                                   "k_rows<FmtQ4_K, 8, 3, XL> (down) + k_moe_combine"))
+                                  ("k_moe_down_xl<FmtQ4_K> (down + weighted sum)" if tokens == 1 else
+                                   "k_moe_down_xlt<FmtQ4_K> (down + weighted sum)"))
         base = synth.moe_q4_k(tokens)
         E, D, FF, K = base["n_experts"], base["dim"], base["ff"], base["k"]
         self.E, self.D, self.FF, self.K = E, D, FF, K

@@ -940,6 +940,129 @@ __global__ __launch_bounds__(512) void k_moe_down_xl(RowsArgs a, const float *gw
   }
 }
 
+// k_moe_down_xl for several tokens: workgroup (row block, token), wave j =
+// slot j, nrt row steps of 8 rows per wave (tile t+1's weights in flight while
+// tile t is dotted), so the workgroups cover the rows of every token with one
+// per CU and all K slots' x is staged once per nrt * 8 rows.  With a grid x
+// extent that is a multiple of 8 (16 tokens of 2048 rows: 16 blocks) a block's
+// rows sit on one XCD for every token, so tokens that share an expert read its
+// rows through the same L2.  Every dot has the bits of the per-pair XL launch
+// and the k row values are summed in slot order as k_moe_combine does.
+constexpr int MOE_DOWN_T_MAX_ROWS = 512;  // rows per workgroup (nrt <= 64)
+
+template <class F>
+__global__ __launch_bounds__(512) void k_moe_down_xlt(RowsArgs a, const float *gw, int32_t K, int32_t nrt) {
+  constexpr int NT = 512, LPR = 8, CPL = 3, NCH = LPR * CPL, RPW = 64 / LPR, NDW = F::NDW;
+  constexpr int NSX = F::NS > 0 ? F::NS : 1;
+  constexpr int XS = NCH * 16;                    // 16-byte x segments of one slot
+  constexpr int XSEG = MOE_DOWN_MAX_K * XS / NT;  // staged by each thread
+  static_assert(XSEG * NT == MOE_DOWN_MAX_K * XS, "x staging");
+  static_assert(MOE_DOWN_MAX_K * NCH <= NT, "one thread per (slot, chunk) for the block sums");
+  __shared__ u32x4 xl[MOE_DOWN_MAX_K][NCH * 17];
+  __shared__ float xsl[MOE_DOWN_MAX_K][NCH][NSX];
+  __shared__ float cb[MOE_DOWN_MAX_K][MOE_DOWN_T_MAX_ROWS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gi = lane / LPR, q = lane % LPR;
+  const int tok = blockIdx.y;
+  const int C = a.dim1 >> 6;
+  const int row0 = blockIdx.x * nrt * RPW;
+
+  u32x4a4 xr[XSEG];
+#pragma unroll
+  for (int u = 0; u < XSEG; ++u) {
+    const int g = u * NT + tid, j = g / XS, c = (g % XS) >> 4;
+    const bool in = (j < K) & (c < C);
+    const float *xp = a.x + (int64_t)(tok * K + (in ? j : 0)) * a.x_stride + (int64_t)(in ? c : 0) * 64;
+    xr[u] = ((const u32x4a4 *)xp)[g & 15];
+  }
+  // wave wid's slot (a slot past K loads the tensor's first chunk, masked)
+  const int expert = a.ids[tok * K + (wid < K ? wid : 0)];
+  const bool bad = (wid >= K) | (expert < 0) | (expert >= a.expert_count);
+  const int64_t ebase = bad ? 0 : (int64_t)expert * a.expert_stride;
+  auto load = [&](int t, uint32_t (&D)[CPL][NDW], bool (&ok)[CPL], int64_t (&E)[CPL]) {
+    const int lr = row0 + t * RPW + gi;
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+      const int c = u * LPR + q;
+      ok[u] = !bad && t < nrt && c < C && lr < a.rows;
+      E[u] = a.base0 + ebase + (int64_t)lr * a.row_stride + (int64_t)c * 64;
+      F::load(a.W0, ok[u] ? E[u] : 0, D[u]);
+    }
+  };
+  uint32_t DA[CPL][NDW], DB[CPL][NDW];
+  bool okA[CPL], okB[CPL];
+  int64_t EA[CPL], EB[CPL];
+  load(0, DA, okA, EA);
+#pragma unroll
+  for (int u = 0; u < XSEG; ++u) {
+    const int g = u * NT + tid, j = g / XS, c = (g % XS) >> 4;
+    const uint32_t m = opaque(((j < K) & (c < C)) ? ~0u : 0u);
+    xl[j][c * 17 + (g & 15)] = u32x4{xr[u].x & m, xr[u].y & m, xr[u].z & m, xr[u].w & m};
+  }
+  __syncthreads();
+  auto read_x = [&](int j, int ch, float (&xu)[64]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const u32x4 t = xl[j][ch * 17 + i];
+      xu[4 * i] = __uint_as_float(t.x);
+      xu[4 * i + 1] = __uint_as_float(t.y);
+      xu[4 * i + 2] = __uint_as_float(t.z);
+      xu[4 * i + 3] = __uint_as_float(t.w);
+    }
+  };
+  if constexpr (F::NS > 0) {
+    if (tid < MOE_DOWN_MAX_K * NCH) {
+      const int j = tid / NCH, ch = tid % NCH;
+      float xu[64], su[NSX];
+      read_x(j, ch, xu);
+      F::sums(xu, su);
+#pragma unroll
+      for (int i = 0; i < NSX; ++i) xsl[j][ch][i] = su[i];
+    }
+    __syncthreads();
+  }
+  auto finish = [&](int t, const uint32_t (&D)[CPL][NDW], const bool (&ok)[CPL], const int64_t (&E)[CPL]) {
+    float acc = 0.f;  // the per-pair launch's accumulation, bit for bit
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+      float xu[64], su[NSX];
+      const int ch = (int)opaque((uint32_t)(u * LPR + q));
+      read_x(wid, ch, xu);
+#pragma unroll
+      for (int i = 0; i < NSX; ++i) su[i] = xsl[wid][ch][i];
+      float r = F::dot(D[u], xu, su, E[u]);
+      // one chunk's x in VGPRs at a time
+      asm volatile("" : "+v"(r)::"memory");
+      acc += ok[u] ? r : 0.f;
+    }
+    float v[1] = {acc};
+    const float r = reduce_transpose<1, LPR>(v, lane);
+    if (q == 0) cb[wid][t * RPW + gi] = r;
+  };
+  if (wid < K) {  // wave-uniform
+    for (int t = 0; t < nrt; t += 2) {
+      load(t + 1, DB, okB, EB);
+      __builtin_amdgcn_sched_barrier(0);
+      finish(t, DA, okA, EA);
+      __builtin_amdgcn_sched_barrier(0);
+      load(t + 2, DA, okA, EA);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 1 < nrt) finish(t + 1, DB, okB, EB);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __syncthreads();
+  for (int r = tid; r < nrt * RPW; r += NT) {
+    const int row = row0 + r;
+    if (row < a.rows) {
+      float out = 0.f;
+      for (int j = 0; j < K; ++j) out = rounded(gw[tok * K + j] * cb[j][r]) + out;
+      a.y[(int64_t)tok * a.y_stride + row] = out;
+    }
+  }
+}
+
 // Y[t*dim + r] = sum_j w[t,j] * ys[(t*K + j)*dim + r] in j order, a*d + out like
 // saxpyInPlace (MutableFloatTensor.kt:61-66).
 __global__ void k_moe_combine(const float *ys, const float *w, int32_t T, int32_t K, int32_t dim, float *Y) {
@@ -1399,9 +1522,25 @@ static hipError_t launch_moe_down_cfg(const RowsArgs &a, const float *gw, int32_
     hipLaunchKernelGGL((k_moe_down<F, LPR, 8>), dim3((unsigned)n8, T), dim3(512), 0, s, a, gw, K);
     return hipGetLastError();
   }
-  if (n4 * T > 2 * (int64_t)dev.cu_count) return hipErrorNotSupported;
-  hipLaunchKernelGGL((k_moe_down<F, LPR, 4>), dim3((unsigned)n4, T), dim3(256), 0, s, a, gw, K);
-  return hipGetLastError();
+  if (n4 * T <= 2 * (int64_t)dev.cu_count) {
+    hipLaunchKernelGGL((k_moe_down<F, LPR, 4>), dim3((unsigned)n4, T), dim3(256), 0, s, a, gw, K);
+    return hipGetLastError();
+  }
+  // more tokens, rows of 17..24 chunks: row steps of 8 rows looped per wave,
+  // about one workgroup per CU over all tokens
+  if constexpr (F::NDW <= 20) {
+    if (a.dim1 > 16 * 64 && a.dim1 <= 24 * 64) {
+      const int64_t steps = (a.rows + 7) / 8;
+      int64_t nrt = (steps * T + dev.cu_count - 1) / dev.cu_count;
+      if (nrt < 1) nrt = 1;
+      if (nrt * 8 <= MOE_DOWN_T_MAX_ROWS) {
+        const int64_t nb = (steps + nrt - 1) / nrt;
+        hipLaunchKernelGGL(k_moe_down_xlt<F>, dim3((unsigned)nb, T), dim3(512), 0, s, a, gw, K, (int32_t)nrt);
+        return hipGetLastError();
+      }
+    }
+  }
+  return hipErrorNotSupported;
 }
 
 template <class F>

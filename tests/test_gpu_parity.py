@@ -637,6 +637,52 @@ def test_moe_batch_equals_tokens_alone(g4, ctx, oracle, fmt):
     assert_dots(Yb.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe batch")
 
 
+@pytest.mark.parametrize("fmt,T,K,D", [(Q4_K, 16, 8, 512), (Q4_K, 5, 3, 512), (Q4_K, 39, 8, 512),
+                                       (Q4_K, 7, 1, 100), (Q4_0, 24, 8, 256), (Q8_0, 33, 6, 192),
+                                       (Q5_K, 9, 8, 128)])
+def test_moe_fused_down_tokens(g4, ctx, oracle, fmt, T, K, D):
+    """Down rows of 17..24 chunks (ff = 1408 here) for 2..39 tokens: one launch
+    does the down projection and the weighted sum, workgroup (row block, token)
+    with one wave per slot and several 8-row steps per wave (partial last blocks,
+    idle slot waves for k < 8, rows that end inside a step at D = 100).  Within
+    the bound of the oracle, every token's output bit-equal to the token run
+    alone (whose down projection is the one-token fused launch), and out-of-range
+    ids add zero rows."""
+    import torch
+    announce("moe fused down fmt=%d T=%d K=%d D=%d" % (fmt, T, K, D))
+    E, FF = 12, 1408
+    gu = synth.weights(61, "gu%d" % D, fmt, E * 2 * FF * D)
+    dn = synth.weights(61, "dn%d" % D, fmt, E * D * FF)
+    lg = synth.activations(61, "lg%d.%d" % (T, K), T * E).reshape(T, E)
+    X = synth.activations(61, "X%d.%d" % (T, D), T * D).reshape(T, D)
+    wgu = upload(g4, ctx, fmt, gu, E * 2 * FF * D)
+    wdn = upload(g4, ctx, fmt, dn, E * D * FF)
+    Yb, idb, wb = g4.moe_routed(ctx, wgu, wdn, X, lg, K, True, D, FF)
+    y64, bound = oracle.moe_exact(fmt, gu, fmt, dn, X, idb, wb, D, FF)
+    assert_dots(Yb.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe fused down")
+    for t in sorted({0, T // 2, T - 1}):
+        Y1, id1, w1 = g4.moe_routed(ctx, wgu, wdn, X[t:t + 1], lg[t:t + 1], K, True, D, FF)
+        assert np.array_equal(id1[0], idb[t]) and same_bits(w1[0], wb[t]), t
+        assert same_bits(Y1[0], Yb[t]), t
+    bad = idb.copy()
+    bad[0, K - 1] = -1
+    bad[T - 1, 0] = E
+    d_Y = torch.full((T, D), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    try:
+        g4.moe_dev(ctx, wgu, wdn, torch.from_numpy(X).cuda(), T, D, FF, torch.from_numpy(bad).cuda(),
+                   torch.from_numpy(wb).cuda(), K, d_Y)
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_stream(None)
+    ids0, w0 = bad.copy(), wb.copy()
+    off = (bad < 0) | (bad >= E)
+    ids0[off] = 0
+    w0[off] = 0.0
+    y64, bound = oracle.moe_exact(fmt, gu, fmt, dn, X, ids0, w0, D, FF)
+    assert_dots(d_Y.cpu().numpy().reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe fused down, bad ids")
+
+
 @pytest.mark.parametrize("case", ["t64", "t80_e8", "ff384", "nonfinite", "ref_gates"])
 def test_moe_grouped_by_expert(g4, ctx, oracle, case):
     """Calls of 40 or more Q4_K tokens run each expert once for all of its (token,
