@@ -565,7 +565,10 @@ int moe_dev(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t n_e
   a.x_div = k;
   a.y = d_h;
   a.y_stride = ff;
-  G4_TRY(launch_status(g4::launch_rows(wgu->type, g4::EPI_GELU_PAIR, a, S, ctx->dev, d_gu, ctx->stream), "moe"));
+  // several tokens: one wave per slot, so a token's x and routing serve its k slots
+  hipError_t egu = g4::launch_moe_gate_up(wgu->type, a, T, ctx->dev, ctx->stream);
+  if (egu == hipErrorNotSupported) egu = g4::launch_rows(wgu->type, g4::EPI_GELU_PAIR, a, S, ctx->dev, d_gu, ctx->stream);
+  G4_TRY(launch_status(egu, "moe"));
   g4::RowsArgs b;
   memset(&b, 0, sizeof(b));
   b.W0 = b.W1 = wdn->d;

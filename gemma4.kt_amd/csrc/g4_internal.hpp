@@ -141,12 +141,17 @@ hipError_t launch_argmax(const float *v, int32_t n, float *part_val, int32_t *pa
 constexpr int ROUTE_LAUNCH_MAX_E = 1024;
 hipError_t launch_route(const float *logits, int32_t T, int32_t n_experts, int32_t k, int32_t renorm,
                         const float *expert_scale, int32_t *ids, float *weights, hipStream_t stream);
-// Down projection and weighted sum of the routed experts in one launch for few
-// tokens (row tiles x tokens <= 2 per CU, k = 1..8, one column pass of at most
-// 2048 columns, rows on the 64-element fast path); hipErrorNotSupported otherwise
-// (the caller then uses launch_rows + launch_moe_combine).
+// Down projection and weighted sum of the routed experts in one launch (k =
+// 1..8, one column pass of at most 2048 columns, rows on the 64-element fast
+// path; one token, or rows of 17..24 chunks for more); hipErrorNotSupported
+// otherwise (the caller then uses launch_rows + launch_moe_combine).
 hipError_t launch_moe_down(int type, const RowsArgs &a, const float *gw, int32_t T, int32_t K, const DevInfo &dev,
                            hipStream_t s);
+// Gate+up (EPI_GELU_PAIR, routing inside when a.route_logits) of T >= 2 tokens
+// with one wave per slot (a.x_div = k <= 8) and one workgroup per (row block,
+// token), for Q8_0/Q4_0/Q4_K/Q5_K/Q6_K rows of 17..32 chunks on the fast path;
+// hipErrorNotSupported otherwise (the caller then uses launch_rows).
+hipError_t launch_moe_gate_up(int type, const RowsArgs &a, int32_t T, const DevInfo &dev, hipStream_t s);
 // dst = src for `bytes` (a multiple of 4; both ends 16-byte aligned), by a kernel.
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 // dst[0 .. bytes) = 0 by a kernel (any alignment and size).

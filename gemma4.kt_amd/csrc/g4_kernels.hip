@@ -109,12 +109,14 @@ struct RouteLds {
   float w_out[MAXE];
   uint32_t gmax[ROUTE_FILTER_MAX_K];
   int32_t n_cand;
-  float wm[4];
+  float wm[8];
 };
 
 // Leaves pick k's expert in r.pick_i[k] and its final weight in r.w_out[k],
 // visible to every thread of the block on return (E <= MAXE, K <= E; every
-// thread calls, uniform control flow).
+// thread calls, uniform control flow).  Written for 256 threads; a 512-thread
+// block may call it when E <= 256 (threads from 256 on then hold no logits and
+// take no element in any loop).
 template <int MAXE>
 G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *expert_scale, RouteLds<MAXE> &r) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -147,6 +149,7 @@ G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *
   if (lane == 0) r.wm[wid] = m;
   __syncthreads();
   m = java_max(java_max(r.wm[0], r.wm[1]), java_max(r.wm[2], r.wm[3]));
+  if (blockDim.x > 256) m = java_max(m, java_max(java_max(r.wm[4], r.wm[5]), java_max(r.wm[6], r.wm[7])));
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
     const int i = tid + 256 * u;
@@ -298,7 +301,8 @@ G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *
 
 // --------------------------------------------------------------- engine ----
 
-template <class F, int LPR, int CPL, int EPI, bool MULTI, bool NORM, bool ROUTE = false, bool XL = false, int WPB = 4>
+template <class F, int LPR, int CPL, int EPI, bool MULTI, bool NORM, bool ROUTE = false, bool XL = false, int WPB = 4,
+          bool SLOTW = false>
 __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
   constexpr int NT = 64 * WPB;                   // threads per workgroup (WPB waves)
   constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1;  // row steps per tile (about F::RT chunk loads per lane)
@@ -321,6 +325,12 @@ __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
   // (rows of 17..24 chunks, e.g. 1408 columns, keep 22 of 24 lanes busy rather
   // than 22 of 32); the block sums of x are computed once into LDS
   static_assert(!XL || (EPI == EPI_STORE && !MULTI && !NORM && !ROUTE), "x at use: plain single-pass launches");
+  // SLOTW (MoE gate+up of several tokens): workgroup (row block, token), wave j
+  // takes slot j's expert over the block's rows; the token's x is staged and
+  // routed once for its K <= 8 slots, and a row block's workgroups of every
+  // token run side by side (with a grid x extent that is a multiple of 8, on one
+  // XCD), so tokens that share an expert read its rows through one L2
+  static_assert(!SLOTW || (EPI == EPI_GELU_PAIR && !MULTI && !NORM && !XL && WPB == 8), "slot per wave: gate+up");
   constexpr int NSX = F::NS > 0 ? F::NS : 1;
   // x layout in LDS (16-byte slots): chunk ch's segment i sits at slot
   // ch * 16 + (i ^ (ch & 15)) -- the 8 lanes one LDS cycle serves read 8
@@ -338,7 +348,7 @@ __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
   const int gi = lane / LPR, q = lane % LPR;
   const int seg = blockIdx.y;
   const int C = a.dim1 >> 6;
-  const float *x = a.x + (int64_t)(seg / a.x_div) * a.x_stride;
+  const float *x = a.x + (int64_t)(SLOTW ? seg : seg / a.x_div) * a.x_stride;
   // x of a column pass, staged once per workgroup: each thread fetches XSEG
   // 16-byte segments (coalesced); with the fused norm also the norm weights
   u32x4a4 xr[XSEG];
@@ -359,23 +369,30 @@ __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
     // the token's routing, computed by every workgroup of its segments (the
     // logits are 4 bytes per expert; a separate launch would cost more)
     __shared__ RouteLds<ROUTE_FUSED_MAX_E> rl;
-    const int tok = seg / a.x_div, slot = seg % a.x_div;
+    const int tok = SLOTW ? seg : seg / a.x_div, slot = SLOTW ? min(wid, a.x_div - 1) : seg % a.x_div;
     route_token(a.route_logits + (int64_t)tok * a.route_e, a.route_e, a.x_div, a.route_renorm, a.route_scale, rl);
     expert = __builtin_amdgcn_readfirstlane(rl.pick_i[slot]);
-    if (blockIdx.x == 0 && tid == 0) a.route_ids[seg] = expert, a.route_w[seg] = rl.w_out[slot];
+    if constexpr (SLOTW) {
+      if (blockIdx.x == 0 && lane == 0 && wid < a.x_div)
+        a.route_ids[tok * a.x_div + wid] = expert, a.route_w[tok * a.x_div + wid] = rl.w_out[wid];
+    } else {
+      if (blockIdx.x == 0 && tid == 0) a.route_ids[seg] = expert, a.route_w[seg] = rl.w_out[slot];
+    }
   } else if (a.ids) {
-    expert = a.ids[seg];
+    expert = a.ids[SLOTW ? seg * a.x_div + min(wid, a.x_div - 1) : seg];
   }
   const bool bad_expert = (ROUTE || a.ids) && (expert < 0 || expert >= a.expert_count);
   const int64_t ebase = bad_expert ? 0 : (int64_t)expert * a.expert_stride;
-  float *y = a.y ? a.y + (int64_t)seg * a.y_stride : nullptr;
+  float *y = a.y ? a.y + (int64_t)(SLOTW ? seg * a.x_div + wid : seg) * a.y_stride : nullptr;
 
   const int n_tiles = (a.rows + LRT - 1) / LRT;
   // wave wid of block b is virtual wave wid * blocks + b: when there are fewer
-  // tiles than waves, every workgroup (so every CU) still gets some
-  const int nwv = gridDim.x * wpb, wv = wid * gridDim.x + blockIdx.x;
+  // tiles than waves, every workgroup (so every CU) still gets some.  SLOTW:
+  // every wave of block b takes block b's tiles (for its own slot); waves past
+  // the token's K slots take none
+  const int nwv = SLOTW ? gridDim.x : gridDim.x * wpb, wv = SLOTW ? blockIdx.x : wid * gridDim.x + blockIdx.x;
   const int tpw = (n_tiles + nwv - 1) / nwv;
-  const int t0 = min(n_tiles, wv * tpw), t1 = min(n_tiles, t0 + tpw);
+  const int t0 = min(n_tiles, wv * tpw), t1 = SLOTW && wid >= a.x_div ? t0 : min(n_tiles, t0 + tpw);
   const int passes = MULTI ? (C + LPR * CPL - 1) / (LPR * CPL) : 1;
 
   // row (logical index, matrix, base) of tile t, step k for this lane's group
@@ -616,7 +633,9 @@ __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
     }
   }
 
-  if constexpr (EPI == EPI_GELU_PAIR) {
+  if constexpr (SLOTW) {
+    gq_flush();  // every wave writes its own slot's rows
+  } else if constexpr (EPI == EPI_GELU_PAIR) {
     // The rows still queued when the tiles run out: when the four waves' rows
     // fit in 64 lanes, one wave evaluates them all (one double-precision gelu
     // pass per workgroup instead of one per wave at the kernel's tail).
@@ -1564,6 +1583,38 @@ hipError_t launch_moe_down(int type, const RowsArgs &a, const float *gw, int32_t
     case T_F16: return launch_moe_down_t<FmtHalf<T_F16>>(a, gw, T, K, dev, s);
     case T_BF16: return launch_moe_down_t<FmtHalf<T_BF16>>(a, gw, T, K, dev, s);
     case T_F32: return launch_moe_down_t<FmtF32>(a, gw, T, K, dev, s);
+    default: return hipErrorNotSupported;
+  }
+}
+
+template <class F>
+static hipError_t launch_moe_gate_up_t(const RowsArgs &a, int32_t T, const DevInfo &dev, hipStream_t s) {
+  constexpr int LRT = F::RT;  // logical rows per paired tile at 32 lanes per row
+  const int64_t n_tiles = (a.rows + LRT - 1) / LRT;
+  // one 8-wave workgroup per CU over all tokens
+  int64_t nb = dev.cu_count / T;
+  if (nb > n_tiles) nb = n_tiles;
+  if (nb < 1) nb = 1;
+  if (a.route_logits)
+    hipLaunchKernelGGL((k_rows<F, 32, 1, EPI_GELU_PAIR, false, false, true, false, 8, true>), dim3((unsigned)nb, T),
+                       dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_rows<F, 32, 1, EPI_GELU_PAIR, false, false, false, false, 8, true>), dim3((unsigned)nb, T),
+                       dim3(512), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_gate_up(int type, const RowsArgs &a, int32_t T, const DevInfo &dev, hipStream_t s) {
+  const int C = a.dim1 / 64;
+  if (T < 2 || a.x_div < 1 || a.x_div > 8 || a.norm_w || C <= 16 || C > 32 || !rows_fast_ok(type, a, true))
+    return hipErrorNotSupported;
+  if (a.route_logits && a.route_e > ROUTE_FUSED_MAX_E) return hipErrorNotSupported;
+  switch (type) {
+    case T_Q8_0: return launch_moe_gate_up_t<FmtQ8_0>(a, T, dev, s);
+    case T_Q4_0: return launch_moe_gate_up_t<FmtQ4_0>(a, T, dev, s);
+    case T_Q4_K: return launch_moe_gate_up_t<FmtQ4_K>(a, T, dev, s);
+    case T_Q5_K: return launch_moe_gate_up_t<FmtQ5_K>(a, T, dev, s);
+    case T_Q6_K: return launch_moe_gate_up_t<FmtQ6_K>(a, T, dev, s);
     default: return hipErrorNotSupported;
   }
 }

@@ -683,6 +683,40 @@ def test_moe_fused_down_tokens(g4, ctx, oracle, fmt, T, K, D):
     assert_dots(d_Y.cpu().numpy().reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe fused down, bad ids")
 
 
+@pytest.mark.parametrize("fmt,T,K,D,E,case", [(Q4_K, 16, 8, 2048, 32, ""), (Q4_K, 2, 1, 1088, 16, ""),
+                                              (Q4_K, 39, 3, 2048, 16, ""), (Q8_0, 5, 8, 1088, 8, ""),
+                                              (Q4_0, 16, 8, 2048, 256, ""), (Q5_K, 7, 6, 1536, 16, ""),
+                                              (Q6_K, 3, 8, 2048, 16, ""), (Q4_K, 6, 4, 2048, 16, "nan")])
+def test_moe_gate_up_slot_waves(g4, ctx, oracle, fmt, T, K, D, E, case):
+    """Gate+up of 2 or more tokens with rows of 17..32 chunks: workgroup (row
+    block, token), one wave per slot, routing once per workgroup in 512 threads
+    (up to 256 experts; "nan": a NaN logit, the reference's scans).  The routing
+    equals the oracle's exactly, the output is within the oracle's bound, equal
+    bit for bit to routing first and then g4_moe (the ids path of the same
+    launch) and, per token, to the token run alone (the per-pair launch)."""
+    announce("moe gate+up slot waves fmt=%d T=%d K=%d D=%d E=%d %s" % (fmt, T, K, D, E, case))
+    FF = 256
+    gu = synth.weights(62, "gu%d.%d" % (D, E), fmt, E * 2 * FF * D)
+    dn = synth.weights(62, "dn%d.%d" % (D, E), fmt, E * D * FF)
+    lg = synth.activations(62, "lg%d.%d.%d" % (T, K, E), T * E).reshape(T, E)
+    X = synth.activations(62, "X%d.%d" % (T, D), T * D).reshape(T, D)
+    if case == "nan":
+        lg[1, 5] = np.nan
+    wgu = upload(g4, ctx, fmt, gu, E * 2 * FF * D)
+    wdn = upload(g4, ctx, fmt, dn, E * D * FF)
+    Yr, idr, wr = g4.moe_routed(ctx, wgu, wdn, X, lg, K, True, D, FF)
+    rids, rw = oracle.route(lg, K, True)
+    assert np.array_equal(idr, rids) and same_bits(wr, rw)
+    Y = g4.moe(ctx, wgu, wdn, X, rids, rw, D, FF)
+    assert same_bits(Yr, Y)
+    y64, bound = oracle.moe_exact(fmt, gu, fmt, dn, X, rids, rw, D, FF)
+    assert_dots(Yr.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe gate+up slot waves")
+    for t in sorted({0, T - 1}):
+        Y1, id1, w1 = g4.moe_routed(ctx, wgu, wdn, X[t:t + 1], lg[t:t + 1], K, True, D, FF)
+        assert np.array_equal(id1[0], idr[t]) and same_bits(w1[0], wr[t]), t
+        assert same_bits(Y1[0], Yr[t]), t
+
+
 @pytest.mark.parametrize("case", ["t64", "t80_e8", "ff384", "nonfinite", "ref_gates"])
 def test_moe_grouped_by_expert(g4, ctx, oracle, case):
     """Calls of 40 or more Q4_K tokens run each expert once for all of its (token,
