@@ -271,7 +271,8 @@ class BatchedQ4_K(Workload):
         # splits summed by k_tok_reduce), its HALF form (token rows 8..15 not
         # loaded) up to eight tokens
         self.dominant_name = ("k_rows<FmtQ4_K, 32, EPI_STORE>" if m <= 2 else
-                              "k_tok_q4k<1, 16, true, %s> (bf16x3 MFMA 16x16x32)" % ("true" if m <= 8 else "false"))
+                              "k_tok_q4k<1, 16, true, %s> (bf16x3 MFMA 16x16x32)" % (
+                                  "true, false" if m <= 8 else "false, true" if m > 16 else "false, false"))
         self.name = "q4_k_batched_8192x2048_m%d" % m
         R, D = c["dim0"], c["dim1"]
         self.R, self.D = R, D

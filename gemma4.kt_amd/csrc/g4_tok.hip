@@ -16,9 +16,17 @@
 //     dmin*m, or d*sc = dmin*m = 0.  Other all-zero sub-blocks (a constant
 //     q0 != 8 with dmin*m = q0 d*sc) leave a residue of the size of the
 //     rounding of the two sums: a known limit.  The rounding of the sums scales
-//     with |q - 8| rather than with q;
+//     with |q - 8| rather than with q.
+//     Workgroups of four or more row tiles (more than 16 tokens at 8192 rows)
+//     form sum(16(q - 8) x) as sum(16 q x) - sum(128 x) instead: 16 q comes
+//     from the nibble as an e4m3 code (two weights per conversion instead of a
+//     convert per weight and a pack per two), and sum(128 x) is formed once per
+//     wave by the same MFMAs with the weight operand of an all-8 sub-block, so
+//     for q = 8 the two sums are equal bit for bit and their difference, taken
+//     before the scale, is exactly 0.  The rounding of these sums scales with q
+//     and 8 rather than |q - 8|;
 //   * activations: an fp32 x has 24 significant bits and splits exactly into
-//     x1 + x2 + x3, three round-to-nearest bf16 parts of 8 bits each, so three
+//     x1 + x2 + x3, three bf16 parts of 8 significant bits each, so three
 //     MFMAs give sum(q x) with exact products and fp32 accumulation.
 //
 // Work split.  v_mfma_f32_16x16x32_bf16 with A = x parts (16 tokens x 32
@@ -92,6 +100,19 @@ G4_DEV bf16x8 nibbles_bf16(uint32_t v0, uint32_t v1) {
   return r;
 }
 
+// bf16 of 16 q for the 8 nibbles of one K-slice, two per instruction: a nibble
+// byte q (0..15) is the e4m3 code of q * 2^-9 (the subnormal codes and the
+// first normal binade are exactly linear in the code), converted with the scale
+// 2^13.  c0, c1: four nibble bytes each, in column order.
+G4_DEV bf16x8 codes_bf16_16q(uint32_t c0, uint32_t c1) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c0, 8192.0f, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c0, 8192.0f, true);
+  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c1, 8192.0f, false);
+  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c1, 8192.0f, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
 // sc and m of sub-blocks 2(g & 3) and 2(g & 3) + 1 of a super-block head, in
 // bytes 0 and 1 (getScaleMinK4, Q4_KFloatTensor.kt:70-84)
 G4_DEV void scale_min_pair(const u32x4 &H, int g, uint32_t &scp, uint32_t &mp) {
@@ -131,7 +152,11 @@ constexpr int TOK_GPW = 2;
 // by a fixed stride per row tile, and the wave's two groups lie in one
 // super-block, whose head is loaded once and whose four sub-blocks' scales
 // take wave-uniform byte positions.
-template <int TT, int WPB, bool AL, bool HALF>
+// SUB8: the weight operand is 16 q from e4m3 codes (two per instruction), with
+// sum(128 x) formed once per wave and subtracted per sub-block; else 16 (q - 8)
+// from signed bytes (workgroups of few row tiles, where the per-wave sum(128 x)
+// does not repay).
+template <int TT, int WPB, bool AL, bool HALF, bool SUB8>
 __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   constexpr int GPW = TOK_GPW, NH = AL ? 1 : GPW;
   static_assert(TT * GPW <= TOK_SLOTS && WPB >= TT && WPB % TT == 0, "tile shape");
@@ -325,6 +350,26 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
 #pragma unroll
   for (int ti = 0; ti < TT; ++ti)
     if ((j >> 1) >= ng) xsT[ti] = 0.f;  // a group past the slice
+  // SUB8: sum(128 x) of each sub-block with the MFMAs the tiles use (B = 128 is
+  // the weight operand of an all-8 sub-block, bit for bit), subtracted from
+  // each tile's sum(16 q x) before its scale
+  f32x4 S8[SUB8 ? TT : 1][SUB8 ? GPW : 1][2];
+  if constexpr (SUB8) {
+    bf16x8 b128;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) b128[e] = (__bf16)128.0f;
+#pragma unroll
+    for (int ti = 0; ti < TT; ++ti)
+#pragma unroll
+      for (int gi = 0; gi < GPW; ++gi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          S8[ti][gi][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int p = 0; p < 3; ++p)
+            S8[ti][gi][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[ti][gi][h][p], b128, S8[ti][gi][h], 0, 0, 0);
+        }
+  }
 
   // mid() runs between the partial tile's LDS store and the barrier
   auto tile = [&](int rt, const u32x2a4 (&Q)[GPW], const u32x4 (&H)[NH], const int (&gs)[GPW], auto &&mid) {
@@ -368,8 +413,14 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
       for (int gi = 0; gi < GPW; ++gi) {
         if (gi < ng) {  // wave-uniform
           const uint32_t w0 = Q[gi].x, w1 = Q[gi].y;
-          const bf16x8 bl = nibbles_bf16(opaque(lo_nibbles_s16(w0)), opaque(lo_nibbles_s16(w1)));
-          const bf16x8 bh = nibbles_bf16(opaque(hi_nibbles_s16(w0)), opaque(hi_nibbles_s16(w1)));
+          bf16x8 bl, bh;
+          if constexpr (SUB8) {
+            bl = codes_bf16_16q(opaque(w0 & 0x0F0F0F0Fu), opaque(w1 & 0x0F0F0F0Fu));
+            bh = codes_bf16_16q(opaque((w0 >> 4) & 0x0F0F0F0Fu), opaque((w1 >> 4) & 0x0F0F0F0Fu));
+          } else {
+            bl = nibbles_bf16(opaque(lo_nibbles_s16(w0)), opaque(lo_nibbles_s16(w1)));
+            bh = nibbles_bf16(opaque(hi_nibbles_s16(w0)), opaque(hi_nibbles_s16(w1)));
+          }
 #pragma unroll
           for (int ti = 0; ti < TT; ++ti) P[ti][gi][0] = P[ti][gi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -390,8 +441,13 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
           for (int ti = 0; ti < TT; ++ti)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              acc[ti][i] = __builtin_fmaf(d1[2 * gi], P[ti][gi][0][i], acc[ti][i]);
-              acc[ti][i] = __builtin_fmaf(d1[2 * gi + 1], P[ti][gi][1][i], acc[ti][i]);
+              if constexpr (SUB8) {
+                acc[ti][i] = __builtin_fmaf(d1[2 * gi], P[ti][gi][0][i] - S8[ti][gi][0][i], acc[ti][i]);
+                acc[ti][i] = __builtin_fmaf(d1[2 * gi + 1], P[ti][gi][1][i] - S8[ti][gi][1][i], acc[ti][i]);
+              } else {
+                acc[ti][i] = __builtin_fmaf(d1[2 * gi], P[ti][gi][0][i], acc[ti][i]);
+                acc[ti][i] = __builtin_fmaf(d1[2 * gi + 1], P[ti][gi][1][i], acc[ti][i]);
+              }
             }
     }
     // the WPB column slices are summed in wave order (deterministic), the work
@@ -518,14 +574,22 @@ hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_
   // groups lie in one super-block
   // at most 8 tokens: the x loads of tokens 8..15 are left out
   const bool al = (a.base % 256) == 0 && (a.row_stride % 256) == 0 && (a.dim1 % 128) == 0, half = a.M <= 8;
+  // the 16 q operand from four row tiles per workgroup on (8192 x 2048: 32 and 64
+  // tokens 10.58/15.23 -> 10.42/14.73 us; 16 tokens, two tiles, 8.27 -> 8.35)
+  const int n_rt = (a.rows + 15) / 16, rpb = (n_rt + sh.gx - 1) / sh.gx;
+  const bool sub8 = !half && rpb >= 4;
   if (al && half)
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, true, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
+  else if (al && sub8)
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, false, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
   else if (al)
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, false, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
   else if (half)
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, true, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
+  else if (sub8)
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, false, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
   else
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, false, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
   if (sh.splits == 1) return hipGetLastError();
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -452,6 +452,26 @@ def test_integer_dots_exact(g4, ctx, oracle, t, rows, cols):
     w.free()
 
 
+def test_integer_dots_exact_sixteen_q_operands(g4, ctx, oracle):
+    """The matrix-core kernel with five row tiles per workgroup (200 tokens over
+    1280 rows), whose weight operands are 16 q less sum(128 x): integer weights
+    and activations give the exact dots there too."""
+    announce("integer dots batched 16q operands")
+    rows, cols, m = 1280, 2048, 200
+    n = rows * cols
+    raw = _integer_blocks(Q4_K, n, 93)
+    W = oracle.dequant(Q4_K, raw, 0, n).reshape(rows, cols).astype(np.float64)
+    assert np.all(W == np.round(W))
+    X = np.random.default_rng(94).integers(-3, 4, (m, cols)).astype(np.float32)
+    w = upload(g4, ctx, Q4_K, raw, n)
+    Y = w.matmul_batch(X, rows, cols)
+    EX = X.astype(np.float64) @ W.T
+    bad = np.argwhere(Y.astype(np.float64) != EX)
+    assert bad.size == 0, "%d wrong, first %r: %r vs %r" % (len(bad), tuple(bad[0]), Y[tuple(bad[0])],
+                                                           EX[tuple(bad[0])])
+    w.free()
+
+
 # matrix-core multi-token kernel (M >= 3): partial row and token tiles, several
 # column splits (summed by the reduce launch: 4224 and 4096 columns), rows that
 # start mid super-block (1408 = 5.5 super-blocks), a row offset, a single
@@ -473,14 +493,14 @@ def test_q4_k_batched_matrix_core_shapes(g4, ctx, oracle, m, rows, dim1, off_row
         assert_dots(Y[i], ex, ab, "token %d" % i)
 
 
-@pytest.mark.parametrize("rows,dim1", [(40, 2048), (34, 1408)])
-def test_q4_k_batched_matrix_core_non_finite_x(g4, ctx, oracle, rows, dim1):
-    """+inf, NaN and -inf activations in three of five tokens: those tokens' outputs are
+@pytest.mark.parametrize("rows,dim1,m", [(40, 2048, 5), (34, 1408, 5), (1280, 2048, 200)])
+def test_q4_k_batched_matrix_core_non_finite_x(g4, ctx, oracle, rows, dim1, m):
+    """+inf, NaN and -inf activations in three tokens: those tokens' outputs are
     all non-finite, as the reference's are (inf * w and NaN * w reach every row), and
     the finite tokens, which share the kernel's waves with them, stay within the bound.
-    Rows of whole super-blocks (2048) and rows that start mid super-block (1408)."""
-    announce("q4_k batched non-finite x rows=%d dim1=%d" % (rows, dim1))
-    m = 5
+    Rows of whole super-blocks (2048), rows that start mid super-block (1408), and
+    five row tiles per workgroup (the 16 q operands less sum(128 x))."""
+    announce("q4_k batched non-finite x rows=%d dim1=%d m=%d" % (rows, dim1, m))
     raw = synth.weights(54, "mcnf%d" % dim1, Q4_K, rows * dim1)
     X = synth.activations(54, "mcnfx%d" % dim1, m * dim1).reshape(m, dim1)
     X[1, 5] = np.inf

@@ -153,12 +153,15 @@ def test_zero_rows_matvec(g4, ctx, oracle, t, rows, cols):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("t,m", [(Q4_K, 2), (Q4_K, 8), (Q4_K, 33), (Q4_0, 4), (Q5_K, 3)])
-def test_zero_rows_batched(g4, ctx, oracle, t, m):
-    """Several activation rows: the matrix-core kernel for Q4_K (16(q - 8) operands),
-    the row engine per token otherwise."""
-    announce("zero-bound batched type %d M=%d" % (t, m))
-    rows, cols = 96, 2048
+@pytest.mark.parametrize("t,m,rows", [(Q4_K, 2, 96), (Q4_K, 8, 96), (Q4_K, 33, 96), (Q4_0, 4, 96), (Q5_K, 3, 96),
+                                      (Q4_K, 200, 1280)])
+def test_zero_rows_batched(g4, ctx, oracle, t, m, rows):
+    """Several activation rows: the matrix-core kernel for Q4_K (16(q - 8)
+    operands; with 200 tokens over 1280 rows, five row tiles per workgroup, the
+    16 q operands less sum(128 x), whose difference is exactly 0 for q = 8), the
+    row engine per token otherwise."""
+    announce("zero-bound batched type %d M=%d rows=%d" % (t, m, rows))
+    cols = 2048
     kinds = _kinds(rows)
     raw = BUILD[t](rows, cols, kinds)
     X = synth.activations(7, "X%d" % m, m * cols).reshape(m, cols)
