@@ -85,6 +85,27 @@ G4_DEV void split3(const float (&v)[8], bf16x8 &p1, bf16x8 &p2, bf16x8 &p3) {
   p3 = __builtin_bit_cast(bf16x8, c);
 }
 
+// split3 for four values: parts p = 0, 1, 2 as two dwords each (values 0, 1
+// and 2, 3 in the low and high halves), the same parts as split3 gives
+template <bool GUARD>
+G4_DEV void split3_4(const float (&v)[4], u32x2a4 (&pt)[3]) {
+  uint32_t t1[4], t2[4], t3[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    t1[e] = __float_as_uint(v[e]) & 0xFFFF0000u;
+    float r1 = v[e] - __uint_as_float(t1[e]);
+    if (GUARD) r1 = __builtin_isinf(v[e]) ? 0.f : r1;
+    t2[e] = __float_as_uint(r1) & 0xFFFF0000u;
+    t3[e] = __float_as_uint(r1 - __uint_as_float(t2[e]));
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    pt[0][k] = __builtin_amdgcn_perm(t1[2 * k + 1], t1[2 * k], 0x07060302u);
+    pt[1][k] = __builtin_amdgcn_perm(t2[2 * k + 1], t2[2 * k], 0x07060302u);
+    pt[2][k] = __builtin_amdgcn_perm(t3[2 * k + 1], t3[2 * k], 0x07060302u);
+  }
+}
+
 // bf16 of 16(q - 8) for the 8 nibbles of one K-slice.  A nibble q moved to the
 // top of its byte and xored with 0x80 is the signed byte 16(q - 8); it converts
 // to float with one sign-extending byte select and to bf16 exactly.
@@ -273,80 +294,138 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
     load_w(rt0, rt0 < rt1, QA, HA, GA);
   __builtin_amdgcn_sched_barrier(0);
 
-  // back from LDS in the MFMA layout: lane (j, n) takes token n, columns
-  // 64 gi + 32 h + 8 j .. +8 of the slice (the K-slice j of sub-block (gi, h));
-  // a wave reads only what it wrote, and LDS operations of a wave run in order
-  u32x4a4 xr[TT][GPW][2][2];
-  float *xst = (float *)lds + wid * 16 * XROW;
+  float xsT[TT];
+  bf16x8 A[TT][GPW][2][3];
+  if constexpr (HALF) {
+    // At most 8 tokens: the bf16 parts and the sub-block sums are formed from
+    // the x the lanes loaded (tokens 0..7, four columns per lane), so no lane
+    // works on the zero tokens 8..15, then staged in the wave's LDS as
+    // [part][row][128 columns] (rows 0..7 the tokens, row 8 zeros for lanes
+    // 8..15 of the MFMA layout) and read back in that layout.
+    constexpr int XB = 272;                        // one row: 128 bf16 and 16 bytes of padding
+    constexpr int XW = 3 * 9 * XB + 9 * 4 * 4;     // a wave's region: parts, then the sums [9][4]
+    static_assert((size_t)WPB * XW <= XST_BYTES, "x staging");
+    unsigned char *xp = lds + (size_t)wid * XW;
+    float *sxt = (float *)(xp + 3 * 9 * XB);
+    if (lane < 48) *(u32x4 *)(xp + (lane >> 4) * 9 * XB + 8 * XB + 16 * (lane & 15)) = u32x4{0u, 0u, 0u, 0u};
+    if (lane == 48) *(u32x4 *)(sxt + 8 * 4) = u32x4{0u, 0u, 0u, 0u};
+    // lane l holds columns 4c .. 4c + 3 (c = l % 32) of token 2q + l / 32: sub-block
+    // c / 8, whose sum is over the 8 lanes of the group (every lane ends with it)
+    const int c = lane & 31;
+    bool bq = false;
 #pragma unroll
-  for (int ti = 0; ti < TT; ++ti) {
+    for (int q = 0; q < 4; ++q) {
+      float t = __uint_as_float(xg[0][q].x);
+      t += __uint_as_float(xg[0][q].y);
+      t += __uint_as_float(xg[0][q].z);
+      t += __uint_as_float(xg[0][q].w);
+      t = pstep<1>(t);
+      t = pstep<2>(t);
+      t = pstep<4>(t);
+      if ((lane & 7) == 0) sxt[(2 * q + (lane >> 5)) * 4 + (c >> 3)] = t;
+      bq |= !__builtin_isfinite(t);
+    }
+    // the split without the infinity guard runs unless some sum in the wave is
+    // infinite or NaN (wave-uniform)
+    auto split_store = [&](auto guard) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) *(u32x4 *)(xst + (2 * q + (lane >> 5)) * XROW + 4 * (lane & 31)) = xg[ti][q];
+      for (int q = 0; q < 4; ++q) {
+        const float v[4] = {__uint_as_float(xg[0][q].x), __uint_as_float(xg[0][q].y), __uint_as_float(xg[0][q].z),
+                            __uint_as_float(xg[0][q].w)};
+        u32x2a4 pt[3];
+        split3_4<decltype(guard)::value>(v, pt);
+#pragma unroll
+        for (int p = 0; p < 3; ++p) *(u32x2a4 *)(xp + p * 9 * XB + (2 * q + (lane >> 5)) * XB + 8 * c) = pt[p];
+      }
+    };
+    if (__builtin_amdgcn_ballot_w64(bq) != 0)
+      split_store(std::true_type());
+    else
+      split_store(std::false_type());
+    const int row = n < 8 ? n : 8;
+    xsT[0] = sxt[row * 4 + j];
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) xr[ti][gi][h][u] = *(const u32x4 *)(xst + n * XROW + 64 * gi + 32 * h + 8 * j + 4 * u);
-  }
-  __syncthreads();  // every wave has its x: the LDS now holds the partial tiles
+        for (int p = 0; p < 3; ++p)
+          A[0][gi][h][p] = *(const bf16x8 *)(xp + p * 9 * XB + row * XB + 2 * (64 * gi + 32 * h + 8 * j));
+    __syncthreads();  // every wave has its x: the LDS now holds the partial tiles
+  } else {
+    // back from LDS in the MFMA layout: lane (j, n) takes token n, columns
+    // 64 gi + 32 h + 8 j .. +8 of the slice (the K-slice j of sub-block (gi, h));
+    // a wave reads only what it wrote, and LDS operations of a wave run in order
+    u32x4a4 xr[TT][GPW][2][2];
+    float *xst = (float *)lds + wid * 16 * XROW;
+#pragma unroll
+    for (int ti = 0; ti < TT; ++ti) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) *(u32x4 *)(xst + (2 * q + (lane >> 5)) * XROW + 4 * (lane & 31)) = xg[ti][q];
+#pragma unroll
+      for (int gi = 0; gi < GPW; ++gi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) xr[ti][gi][h][u] = *(const u32x4 *)(xst + n * XROW + 64 * gi + 32 * h + 8 * j + 4 * u);
+    }
+    __syncthreads();  // every wave has its x: the LDS now holds the partial tiles
 
-  // Per token tile, the sum of x over sub-block j (group j / 2, half j % 2) for
-  // token n, the fp32 MFMA's A operand: each lane adds its 8 values of each
-  // sub-block, and a transposing butterfly over the four K-slice lanes of the
-  // token leaves sub-block j's sum in row j.  x is not masked: the tokens past M
-  // (token 0's x) only reach their own output rows, which are never stored, and
-  // groups past the slice are never multiplied and get no coefficient.
-  float xsT[TT];
-  bool bad = false;
+    // Per token tile, the sum of x over sub-block j (group j / 2, half j % 2) for
+    // token n, the fp32 MFMA's A operand: each lane adds its 8 values of each
+    // sub-block, and a transposing butterfly over the four K-slice lanes of the
+    // token leaves sub-block j's sum in row j.  x is not masked: the tokens past M
+    // (token 0's x) only reach their own output rows, which are never stored, and
+    // groups past the slice are never multiplied and get no coefficient.
+    bool bad = false;
 #pragma unroll
-  for (int ti = 0; ti < TT; ++ti) {
-    float ps[2 * GPW];
-#pragma unroll
-    for (int gi = 0; gi < GPW; ++gi)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        float t = __uint_as_float(xr[ti][gi][h][0].x);
-        t += __uint_as_float(xr[ti][gi][h][0].y);
-        t += __uint_as_float(xr[ti][gi][h][0].z);
-        t += __uint_as_float(xr[ti][gi][h][0].w);
-        t += __uint_as_float(xr[ti][gi][h][1].x);
-        t += __uint_as_float(xr[ti][gi][h][1].y);
-        t += __uint_as_float(xr[ti][gi][h][1].z);
-        t += __uint_as_float(xr[ti][gi][h][1].w);
-        ps[2 * gi + h] = t;
-      }
-    static_assert(GPW == 2, "four sub-blocks per wave");
-    const float t02 = tstep<32>(ps[0], ps[2], lane), t13 = tstep<32>(ps[1], ps[3], lane);
-    xsT[ti] = tstep<16>(t02, t13, lane);
-    bad |= !__builtin_isfinite(xsT[ti]);
-  }
-  // bf16 parts (A operands).  The split without the infinity guard runs unless
-  // some sum in the wave is infinite or NaN (an activation is, or a sum
-  // overflowed): wave-uniform
-  bf16x8 A[TT][GPW][2][3];
-  auto split_all = [&](auto guard) {
-#pragma unroll
-    for (int ti = 0; ti < TT; ++ti)
+    for (int ti = 0; ti < TT; ++ti) {
+      float ps[2 * GPW];
 #pragma unroll
       for (int gi = 0; gi < GPW; ++gi)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          float v[8];
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            v[4 * u] = __uint_as_float(xr[ti][gi][h][u].x);
-            v[4 * u + 1] = __uint_as_float(xr[ti][gi][h][u].y);
-            v[4 * u + 2] = __uint_as_float(xr[ti][gi][h][u].z);
-            v[4 * u + 3] = __uint_as_float(xr[ti][gi][h][u].w);
-          }
-          split3<decltype(guard)::value>(v, A[ti][gi][h][0], A[ti][gi][h][1], A[ti][gi][h][2]);
+          float t = __uint_as_float(xr[ti][gi][h][0].x);
+          t += __uint_as_float(xr[ti][gi][h][0].y);
+          t += __uint_as_float(xr[ti][gi][h][0].z);
+          t += __uint_as_float(xr[ti][gi][h][0].w);
+          t += __uint_as_float(xr[ti][gi][h][1].x);
+          t += __uint_as_float(xr[ti][gi][h][1].y);
+          t += __uint_as_float(xr[ti][gi][h][1].z);
+          t += __uint_as_float(xr[ti][gi][h][1].w);
+          ps[2 * gi + h] = t;
         }
-  };
-  if (__builtin_amdgcn_ballot_w64(bad) != 0)
-    split_all(std::true_type());
-  else
-    split_all(std::false_type());
+      static_assert(GPW == 2, "four sub-blocks per wave");
+      const float t02 = tstep<32>(ps[0], ps[2], lane), t13 = tstep<32>(ps[1], ps[3], lane);
+      xsT[ti] = tstep<16>(t02, t13, lane);
+      bad |= !__builtin_isfinite(xsT[ti]);
+    }
+    // bf16 parts (A operands).  The split without the infinity guard runs unless
+    // some sum in the wave is infinite or NaN (an activation is, or a sum
+    // overflowed): wave-uniform
+    auto split_all = [&](auto guard) {
+#pragma unroll
+      for (int ti = 0; ti < TT; ++ti)
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              v[4 * u] = __uint_as_float(xr[ti][gi][h][u].x);
+              v[4 * u + 1] = __uint_as_float(xr[ti][gi][h][u].y);
+              v[4 * u + 2] = __uint_as_float(xr[ti][gi][h][u].z);
+              v[4 * u + 3] = __uint_as_float(xr[ti][gi][h][u].w);
+            }
+            split3<decltype(guard)::value>(v, A[ti][gi][h][0], A[ti][gi][h][1], A[ti][gi][h][2]);
+          }
+    };
+    if (__builtin_amdgcn_ballot_w64(bad) != 0)
+      split_all(std::true_type());
+    else
+      split_all(std::false_type());
+  }
 #pragma unroll
   for (int ti = 0; ti < TT; ++ti)
     if ((j >> 1) >= ng) xsT[ti] = 0.f;  // a group past the slice
