@@ -49,21 +49,21 @@ Q8_0, Q4_0, Q4_K = 8, 2, 12
 # Recorded in profiles/hbm_traffic_fetch_write_size.md (same command and kernels).
 # "name:part" keys give the other separately timed launches of a step.
 TRAFFIC_BYTES = {
-    "q4_0_ffn_decode_token": 19185408,
+    "q4_0_ffn_decode_token": 19186432,
     "q4_0_ffn_decode_token:down": 9835392,
     "q8_0_matvec_2048x2048": 4638592,
-    "q8_0_lm_head_262144x2048_argmax": 572046496,
+    "q8_0_lm_head_262144x2048_argmax": 572062368,
     "q4_k_batched_8192x2048_m1": 9671552,
-    "q4_k_batched_8192x2048_m8": 10351232,
-    "q4_k_batched_8192x2048_m32": 12703360,
-    "q4_k_batched_8192x2048_m64": 15849088,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40026304,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 549751360,
+    "q4_k_batched_8192x2048_m8": 10344192,
+    "q4_k_batched_8192x2048_m32": 12710528,
+    "q4_k_batched_8192x2048_m64": 15856384,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40018112,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 479384304,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t128": 987322060,
-    "q5_k_matvec_8192x2048": 11776768,
-    "q6_k_matvec_8192x2048": 14137984,
-    "q4_0_ffn_block_decode_token": 29148672,
-    "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572373568,
+    "q5_k_matvec_8192x2048": 11777024,
+    "q6_k_matvec_8192x2048": 14138240,
+    "q4_0_ffn_block_decode_token": 29151872,
+    "q8_0_lm_head_262144x2048_norm_softcap_argmax": 572338944,
     "attention_decode_h16_kv8_d256_len8192": 136771584,
 }
 
