@@ -146,6 +146,47 @@ def test_grouped_moe_replays(g4, request, shape):
         c.close()
 
 
+def test_multi_token_moe_replays(g4, wide_moe_weights):
+    """16 tokens at dim 2048 / ff 1408 take the gate+up launch with one wave per
+    slot (routing in 512 threads) and the down launch that loops 8-row steps and
+    does the weighted sum.  Captured once and replayed three times, with eager
+    one-token and grouped calls between the replays: every replay gives the
+    eager bits, ids and weights."""
+    announce("capture: multi-token MoE replays")
+    mw = wide_moe_weights
+    c = g4.Context(0)
+    stream = torch.cuda.Stream()
+    try:
+        mid = _io(mw, 16, 7)
+        one = _io(mw, 1, 8)
+        big = _io(mw, 96, 9)
+        _moe(g4, c, mw, 96, big)  # eager: sizes the scratch
+        _moe(g4, c, mw, 16, mid)
+        _moe(g4, c, mw, 1, one)
+        torch.cuda.synchronize()
+        want, want_ids, want_w = mid[4].clone(), mid[2].clone(), mid[3].clone()
+        want_one, want_big = one[4].clone(), big[4].clone()
+        mid[4].fill_(float("nan"))
+        mid[2].fill_(-1)
+        g = _capture(c, stream, lambda: _moe(g4, c, mw, 16, mid))
+        for rep in range(3):
+            mid[4].fill_(float("nan"))
+            mid[2].fill_(-1)
+            mid[3].fill_(0.0)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(mid[4], want), "replay %d" % rep
+            assert torch.equal(mid[2], want_ids) and torch.equal(mid[3], want_w), "replay %d" % rep
+            _moe(g4, c, mw, 1, one)
+            _moe(g4, c, mw, 96, big)
+            torch.cuda.synchronize()
+            assert torch.equal(one[4], want_one) and torch.equal(big[4], want_big)
+    finally:
+        torch.cuda.synchronize()
+        c.close()
+
+
 def test_growth_under_capture_is_refused_and_reserve_fixes_it(g4, moe_weights):
     announce("capture: growth refused, then reserved")
     mw = moe_weights
