@@ -17,8 +17,9 @@
 //     q0 != 8 with dmin*m = q0 d*sc) leave a residue of the size of the
 //     rounding of the two sums: a known limit.  The rounding of the sums scales
 //     with |q - 8| rather than with q.
-//     Workgroups of four or more row tiles (more than 16 tokens at 8192 rows)
-//     form sum(16(q - 8) x) as sum(16 q x) - sum(128 x) instead: 16 q comes
+//     Calls of at most 8 tokens and workgroups of four or more row tiles (more
+//     than 16 tokens at 8192 rows) form sum(16(q - 8) x) as
+//     sum(16 q x) - sum(128 x) instead: 16 q comes
 //     from the nibble as an e4m3 code (two weights per conversion instead of a
 //     convert per weight and a pack per two), and sum(128 x) is formed once per
 //     wave by the same MFMAs with the weight operand of an all-8 sub-block, so
@@ -175,10 +176,15 @@ constexpr int TOK_GPW = 2;
 // take wave-uniform byte positions.
 // SUB8: the weight operand is 16 q from e4m3 codes (two per instruction), with
 // sum(128 x) formed once per wave and subtracted per sub-block; else 16 (q - 8)
-// from signed bytes (workgroups of few row tiles, where the per-wave sum(128 x)
-// does not repay).
-template <int TT, int WPB, bool AL, bool HALF, bool SUB8>
+// from signed bytes (9 to 16 tokens in workgroups of few row tiles, where the
+// per-wave sum(128 x) does not repay; with at most 8 tokens it does, its MFMAs
+// running while the first tile's weights are in flight).
+// FULL (with AL): every wave's column slice is whole and the row tiles are
+// whole, so the slice and row checks drop out, and the output offsets within
+// 16 tokens fit 32 bits.
+template <int TT, int WPB, bool AL, bool HALF, bool SUB8, bool FULL>
 __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
+  static_assert(!FULL || AL, "FULL takes the AL layout");
   constexpr int GPW = TOK_GPW, NH = AL ? 1 : GPW;
   static_assert(TT * GPW <= TOK_SLOTS && WPB >= TT && WPB % TT == 0, "tile shape");
   static_assert(!HALF || TT == 1, "HALF: one token tile of at most 8 tokens");
@@ -197,7 +203,7 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   const int n = lane & 15, j = lane >> 4;
   const int C = a.dim1 >> 6;
   const int g0 = ((int)blockIdx.y * WPB + wid) * GPW;  // first group of this wave's slice (even)
-  const int ng = max(0, min(GPW, C - g0));                   // wave-uniform
+  const int ng = FULL ? GPW : max(0, min(GPW, C - g0));      // wave-uniform
   const int tt0 = (int)blockIdx.z * TT;                      // first token tile
   const int n_rt = (a.rows + 15) >> 4;
   const int rpb = (n_rt + gridDim.x - 1) / gridDim.x;
@@ -248,7 +254,18 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
   // lane takes its row's head and its K-slice of both groups
   unsigned char *wst = lds + RED_BYTES + (size_t)wid * 16 * WROW;
   const uint8_t *w_tile0 = a.W + ((a.base >> 8) + (int64_t)(rt0 * 16 + (lane >> 2)) * rs_sb + (g0 >> 2)) * 144;
+  const uint32_t lane_h = (uint32_t)((lane >> 2) * rs_sb * 144) + 4u * (lane & 3);
+  const uint32_t lane_w = lane_h + 16u + 32u * (g0 & 3) + 12u * (lane & 3);
   auto load_raw = [&](int rt, bool live, u32x4 &QR, uint32_t &HR) {
+    if constexpr (FULL && HALF) {
+      // a wave-uniform tile base and this lane's 32-bit offset in it; a tile past
+      // the end reads the matrix's first 16 rows.  (With more tokens this form
+      // measured slower: 32 and 64 tokens 10.3/14.3 -> 10.5/15.1 us.)
+      const uint8_t *tb = a.W + ((a.base >> 8) + (int64_t)((live ? rt : 0) * 16) * rs_sb + (g0 >> 2)) * 144;
+      QR = *(const u32x4 *)(tb + lane_w);
+      HR = *(const uint32_t *)(tb + lane_h);
+      return;
+    }
     // rows past the end read the tensor's first super-block
     const bool ok = live && ng > 0 && rt * 16 + (lane >> 2) < a.rows;
     const uint8_t *sb = ok ? w_tile0 + (int64_t)(rt - rt0) * w_step : a.W;
@@ -540,6 +557,17 @@ __global__ __launch_bounds__(WPB * 64) void k_tok_q4k(TokArgs a) {
       constexpr int WPT = WPB / TT;  // waves per token tile
       const int ti = wid / WPT, c = wid % WPT;
       const int r = rt * 16 + n;
+      if constexpr (FULL && WPT >= 4) {
+        if (c < 4) {  // wave-uniform: component c of every lane's four outputs
+          const float *rp = (const float *)&red[buf][ti][0][lane] + c;
+          float s = rp[0];
+#pragma unroll
+          for (int w = 1; w < WPB; ++w) s += rp[w * 64 * 4];
+          const int m = (tt0 + ti) * 16 + 4 * j + c;
+          float *ob = out + ((int64_t)((tt0 + ti) * 16 + c) * out_stride + rt * 16);
+          if (m < a.M) ob[(uint32_t)(4 * j * out_stride + n)] = s;
+        }
+      } else
       for (int i = c; i < 4; i += WPT) {  // wave-uniform: one component per read, no selects
         const float *rp = (const float *)&red[buf][ti][0][lane] + i;
         float s = rp[0];
@@ -654,21 +682,34 @@ hipError_t launch_tok(int type, const TokArgs &a, const DevInfo &dev, hipStream_
   // at most 8 tokens: the x loads of tokens 8..15 are left out
   const bool al = (a.base % 256) == 0 && (a.row_stride % 256) == 0 && (a.dim1 % 128) == 0, half = a.M <= 8;
   // the 16 q operand from four row tiles per workgroup on (8192 x 2048: 32 and 64
-  // tokens 10.58/15.23 -> 10.42/14.73 us; 16 tokens, two tiles, 8.27 -> 8.35)
+  // tokens 10.58/15.23 -> 10.42/14.73 us; 16 tokens, two tiles, 8.27 -> 8.35),
+  // and with at most 8 tokens (7.13 -> 6.86 us)
   const int n_rt = (a.rows + 15) / 16, rpb = (n_rt + sh.gx - 1) / sh.gx;
-  const bool sub8 = !half && rpb >= 4;
-  if (al && half)
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, true, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
+  const bool sub8 = half || rpb >= 4;
+  // FULL: whole slices and row tiles, 32-bit offsets within a tile and within 16
+  // tokens of the output (8 / 32 / 64 tokens 6.86 / 10.49 / 14.75 -> 6.77 / 10.24 /
+  // 14.29 us)
+  const int64_t ost = sh.splits == 1 ? a.y_stride : a.rows;
+  const bool full = al && (a.dim1 % (64 * TOK_GPW * TOK_WPB)) == 0 && (a.rows % 16) == 0 &&
+                    16 * (a.row_stride / 256) * 144 < (1ll << 31) && 16 * ost < (1ll << 29);
+  if (full && half)
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, true, true, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
+  else if (full && sub8)
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, false, true, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
+  else if (full)
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, false, false, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
+  else if (al && half)
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, true, true, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
   else if (al && sub8)
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, false, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, false, true, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
   else if (al)
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, false, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, true, false, false, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
   else if (half)
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, true, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, true, true, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
   else if (sub8)
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, false, true>), grid, dim3(TOK_WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, false, true, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
   else
-    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, false, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((k_tok_q4k<TOK_TT, TOK_WPB, false, false, false, false>), grid, dim3(TOK_WPB * 64), 0, s, a);
   if (sh.splits == 1) return hipGetLastError();
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
