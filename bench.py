@@ -54,9 +54,9 @@ TRAFFIC_BYTES = {
     "q8_0_matvec_2048x2048": 4638592,
     "q8_0_lm_head_262144x2048_argmax": 572062368,
     "q4_k_batched_8192x2048_m1": 9671552,
-    "q4_k_batched_8192x2048_m8": 10344192,
-    "q4_k_batched_8192x2048_m32": 12710528,
-    "q4_k_batched_8192x2048_m64": 15856384,
+    "q4_k_batched_8192x2048_m8": 10462208,
+    "q4_k_batched_8192x2048_m32": 12698240,
+    "q4_k_batched_8192x2048_m64": 15843968,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40018112,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 479384304,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t128": 987322060,
@@ -269,10 +269,11 @@ class BatchedQ4_K(Workload):
         # one or two tokens: the row-stream kernel (one segment per token); three or
         # more: the matrix-core kernel (one column split up to 2048 columns, more
         # splits summed by k_tok_reduce), its HALF form (token rows 8..15 not
-        # loaded) up to eight tokens
+        # loaded) up to eight tokens; the 16 q operands (SUB8) up to eight tokens and
+        # from four row tiles per workgroup; whole slices and row tiles (FULL) here
         self.dominant_name = ("k_rows<FmtQ4_K, 32, EPI_STORE>" if m <= 2 else
-                              "k_tok_q4k<1, 16, true, %s> (bf16x3 MFMA 16x16x32)" % (
-                                  "true, false" if m <= 8 else "false, true" if m > 16 else "false, false"))
+                              "k_tok_q4k<1, 16, true, %s, true> (bf16x3 MFMA 16x16x32)" % (
+                                  "true, true" if m <= 8 else "false, true" if m > 16 else "false, false"))
         self.name = "q4_k_batched_8192x2048_m%d" % m
         R, D = c["dim0"], c["dim1"]
         self.R, self.D = R, D
