@@ -476,10 +476,14 @@ def test_integer_dots_exact_sixteen_q_operands(g4, ctx, oracle):
 # column splits (summed by the reduce launch: 4224 and 4096 columns), rows that
 # start mid super-block (1408 = 5.5 super-blocks), a row offset, a single
 # 64-column group and several token groups (M = 17, 48, 70); M = 2 takes the
-# row engine, one segment per token
+# row engine, one segment per token.  Whole slices and row tiles (the unchecked
+# form) with column splits: at most 8 tokens (6 x 64 x 4096), three token tiles
+# and three splits behind a row offset (40 x 64 x 6144), and the 16 q operands
+# (32 tokens over 4096 rows: four row tiles per workgroup, two splits)
 @pytest.mark.parametrize("m,rows,dim1,off_rows", [
     (2, 40, 2048, 0), (4, 40, 2048, 0), (17, 34, 4224, 0), (5, 34, 1408, 0), (16, 48, 2048, 3),
-    (3, 20, 64, 0), (48, 40, 2048, 0), (70, 24, 4096, 1)])
+    (3, 20, 64, 0), (48, 40, 2048, 0), (70, 24, 4096, 1), (6, 64, 4096, 0), (40, 64, 6144, 2),
+    (32, 4096, 4096, 0)])
 def test_q4_k_batched_matrix_core_shapes(g4, ctx, oracle, m, rows, dim1, off_rows):
     announce("q4_k batched M=%d rows=%d dim1=%d off_rows=%d" % (m, rows, dim1, off_rows))
     n = (rows + off_rows) * dim1
