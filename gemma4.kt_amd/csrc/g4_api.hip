@@ -474,11 +474,11 @@ int check_moe(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t T
 // Routing done inside the gate+up launch (g4_moe_routed*): the router logits in,
 // the ids and weights it stores out.
 // Calls of at least this many tokens run the experts grouped (launch_moe_grp):
-// measured on the 128-expert top-8 shape, the grouped launches are 3%, 13%, 17%,
-// 36% and 47% faster than the per-pair ones at 40, 48, 56, 128 and 256 tokens,
-// even at 33, and slower at 24 (1.4x) and 16 (2.1x), where an expert has 1.6
-// pairs on average.
-constexpr int32_t MOE_GROUPED_MIN_T = 40;
+// measured on the 128-expert top-8 shape (alternating runs, one box), the grouped
+// launches take 231, 233, 239 and 288 us at 33, 40, 64 and 128 tokens against
+// 261, 260, 374 and 723 us for the per-pair ones, and about 222-230 us from 16 to
+// 32 tokens, where the per-pair ones take 100-193 us.
+constexpr int32_t MOE_GROUPED_MIN_T = 33;
 
 struct MoeRoute {
   const float *d_logits;
@@ -516,7 +516,9 @@ int moe_dev(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t n_e
     gu.x_div = k;
     gu.y = d_h;
     gu.y_stride = ff;
+    gu.gu = d_gu;
     g4::MoeGrpArgs dn = gu;
+    dn.gu = nullptr;
     dn.W = wdn->d;
     dn.base1 = 0;
     dn.row_stride = ff;

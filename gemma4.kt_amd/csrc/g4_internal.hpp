@@ -121,12 +121,19 @@ struct MoeGrpArgs {
   int32_t x_div;
   float *y;
   int64_t y_stride;
+  // gate+up launch: S x 2 rows floats for the gate and up rows of every pair
+  // before gelu (the 16-pair tiles write them here, then k_gelu_mul forms y)
+  float *gu;
 };
 bool moe_grp_ok(int type, const MoeGrpArgs &a);
 // Grants the grouped kernels their largest dynamic LDS size on the current
 // device; called once per device before any launch (g4_open).
 hipError_t moe_grp_init_device();
 hipError_t launch_moe_grp(int type, bool gate_up, const MoeGrpArgs &a, const DevInfo &dev, hipStream_t stream);
+// h[s * h_stride + r] = gelu(gu[s][r]) * gu[s][rows + r] for rows x segments
+// (gu: segments x 2 rows floats, gate then up)
+hipError_t launch_gelu_mul(const float *gu, int32_t rows, int32_t segments, float *h, int64_t h_stride,
+                           hipStream_t stream);
 
 // Plain matvec of rows of 65..256 chunks (g4_wide.hip): the columns split over
 // the waves of a workgroup.  wide_ok: the launch takes it (EPI_STORE, no ids,

@@ -697,6 +697,37 @@ __global__ void k_gelu_mul(const float *gu, int32_t rows, int32_t segments, floa
   }
 }
 
+// k_gelu_mul for rows in fours (16-byte aligned): workgroup (row block, segment),
+// four rows per thread, no index division
+__global__ __launch_bounds__(256) void k_gelu_mul4(const float *gu, int32_t rows, float *h, int64_t h_stride) {
+  const int r = (blockIdx.x * 256 + threadIdx.x) * 4, sg = blockIdx.y;
+  if (r >= rows) return;
+  const float4 g = *(const float4 *)(gu + (int64_t)sg * 2 * rows + r);
+  const float4 u = *(const float4 *)(gu + (int64_t)sg * 2 * rows + rows + r);
+  float4 o;
+  o.x = gelu_ref(g.x) * u.x;
+  o.y = gelu_ref(g.y) * u.y;
+  o.z = gelu_ref(g.z) * u.z;
+  o.w = gelu_ref(g.w) * u.w;
+  *(float4 *)(h + (int64_t)sg * h_stride + r) = o;
+}
+
+hipError_t launch_gelu_mul(const float *gu, int32_t rows, int32_t segments, float *h, int64_t h_stride,
+                           hipStream_t s) {
+  if (rows > 0 && segments > 0 && segments <= 65535 && rows % 4 == 0 && h_stride % 4 == 0 &&
+      ((uintptr_t)gu & 15) == 0 && ((uintptr_t)h & 15) == 0) {
+    hipLaunchKernelGGL(k_gelu_mul4, dim3((unsigned)((rows / 4 + 255) / 256), (unsigned)segments), dim3(256), 0, s,
+                       gu, rows, h, h_stride);
+    return hipGetLastError();
+  }
+  const int64_t n = (int64_t)rows * segments;
+  int blocks = (int)((n + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) return hipSuccess;
+  hipLaunchKernelGGL(k_gelu_mul, dim3(blocks), dim3(256), 0, s, gu, rows, segments, h, h_stride);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- dequant ----
 template <int TYPE>
 __global__ void k_dequant(const uint8_t *W, int64_t offset, int64_t n, float *out) {
@@ -1426,12 +1457,7 @@ hipError_t launch_rows(int type, int epi, const RowsArgs &a, int segments, const
     g.y_stride = 2 * (int64_t)a.rows;
     hipError_t e = launch_generic(type, g, 2, segments, dev, s);
     if (e != hipSuccess) return e;
-    const int64_t n = (int64_t)a.rows * segments;
-    int blocks = (int)((n + 255) / 256);
-    if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(k_gelu_mul, dim3(blocks), dim3(256), 0, s, (const float *)scratch, a.rows, segments, a.y,
-                       a.y_stride);
-    return hipGetLastError();
+    return launch_gelu_mul(scratch, a.rows, segments, a.y, a.y_stride, s);
   }
   if (a.norm_w) return hipErrorInvalidValue;  // callers normalise x first when rows_norm_ok fails
   hipError_t e = launch_generic(type, a, 1, segments, dev, s);

@@ -46,6 +46,7 @@
 #include "g4_device.hpp"
 #include "g4_internal.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace g4 {
@@ -961,6 +962,348 @@ __global__ __launch_bounds__(MG_WPB * 64) void k_moe_grp(MoeGrpArgs a) {
   }
 }
 
+// -------------------------------------------- grouped MoE, 16-pair tiles ----
+// The experts of a multi-token MoE call on k_tok_q4k's tiles.  Workgroup (row
+// block, expert e) takes e's (token, slot) pairs sixteen at a time in pair order
+// (a pass): pair slot t is MFMA row t, its token's x split into bf16 parts in the
+// waves' registers as a 16-token tile (wave w: columns 128 w .. 128 w + 127), and
+// the workgroup walks its 16-row tiles with the 16 q weight operands, each weight
+// read once per pass.  Row r of pair p goes to y[p * y_stride + r]; the gate+up
+// launch runs the expert's gate and up rows as one matrix of 2 ff rows (its two
+// halves adjacent in the slab) and k_gelu_mul forms h.  Workgroups (x,
+// n_experts) write the zero rows of pairs whose id is out of range.  Rows of up
+// to 2048 columns: one column split, no partial sums.
+constexpr int GT_WPB = 16;
+#ifndef GT_GX_PER_CU
+#define GT_GX_PER_CU 1
+#endif
+
+template <bool AL>
+__global__ __launch_bounds__(GT_WPB * 64) void k_grp_q4k(MoeGrpArgs a) {
+  constexpr int WPB = GT_WPB, GPW = TOK_GPW, NH = AL ? 1 : GPW;
+  constexpr int XROW = 132, WROW = 80;
+  constexpr size_t RED_BYTES = sizeof(f32x4) * 2 * WPB * 64, XST_BYTES = sizeof(float) * WPB * 16 * XROW;
+  constexpr size_t WST_BYTES = AL ? (size_t)WPB * 16 * WROW : 0;
+  __shared__ __attribute__((aligned(16))) unsigned char
+      lds[RED_BYTES + WST_BYTES > XST_BYTES ? RED_BYTES + WST_BYTES : XST_BYTES];
+  __shared__ int pl[16];      // the pass's pairs (-1: none)
+  __shared__ int tl[16];      // their tokens (empty slots: the first pair's)
+  __shared__ int wcnt[WPB];   // matches per wave in a scan step
+  f32x4(*red)[WPB][64] = (f32x4(*)[WPB][64])lds;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, j = lane >> 4;
+  const int C = a.dim1 >> 6;
+  const int g0 = wid * GPW;                     // first group of this wave's slice (even)
+  const int ng = max(0, min(GPW, C - g0));      // wave-uniform
+  const int e = blockIdx.y;
+  const bool zero_rows = e == a.n_experts;
+  const int n_rt = (a.rows + 15) >> 4;
+  const int rpb = (n_rt + gridDim.x - 1) / gridDim.x;
+  const int rt0 = min(n_rt, (int)blockIdx.x * rpb), rt1 = min(n_rt, rt0 + rpb);
+  if (rt0 >= rt1) return;  // the whole workgroup
+  const int64_t base = (zero_rows ? 0 : (int64_t)e * a.expert_stride) + a.base0;
+
+  // pairs of rank 16 pass .. 16 pass + 15 among this expert's into pl; returns
+  // the number of its pairs (the same in every thread)
+  auto scan = [&](int pass) {
+    if (tid < 16) pl[tid] = -1;
+    int total = 0;
+    for (int p0 = 0; p0 < a.S; p0 += WPB * 64) {
+      const int p = p0 + tid;
+      bool m = false;
+      if (p < a.S) {
+        const int id = a.ids[p];
+        m = zero_rows ? (id < 0 || id >= a.n_experts) : id == e;
+      }
+      const uint64_t b = __builtin_amdgcn_ballot_w64(m);
+      if (lane == 0) wcnt[wid] = __builtin_popcountll(b);
+      __syncthreads();
+      int before = total, all = 0;
+#pragma unroll
+      for (int w = 0; w < WPB; ++w) {
+        before += w < wid ? wcnt[w] : 0;
+        all += wcnt[w];
+      }
+      const int rank = before + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+      if (m && rank >= 16 * pass && rank < 16 * (pass + 1)) pl[rank - 16 * pass] = p;
+      total += all;
+      __syncthreads();  // wcnt is rewritten next step; pl is complete after the last
+    }
+    if (tid < 16) tl[tid] = (pl[tid] >= 0 ? pl[tid] : pl[0]) / a.x_div;
+    __syncthreads();
+    return total;
+  };
+
+  const int64_t w_step = (16 * a.row_stride >> 8) * 144;  // 16 rows: whole super-blocks
+  // weight group gi of row tile rt, this lane's row (B column n) and K-slice j
+  auto load_w = [&](int rt, bool live, u32x2a4 (&Q)[GPW], u32x4 (&H)[NH], int (&gs)[GPW]) {
+    const int r = rt * 16 + n;
+    const bool rok = live && r < a.rows;
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi) {
+      // rows past the end and groups past the slice read the first group of
+      // the tensor (in bounds; never stored / never multiplied)
+      const int64_t el = (rok && gi < ng) ? base + (int64_t)r * a.row_stride + (int64_t)(g0 + gi) * 64 : 0;
+      const int64_t G = el >> 6;
+      const uint8_t *sb = a.W + (G >> 2) * 144;
+      gs[gi] = (int)(G & 3);
+      H[gi] = *(const u32x4 *)sb;
+      Q[gi] = *(const u32x2a4 *)(sb + 16 + 32 * (G & 3) + 8 * j);
+    }
+  };
+  // AL: a tile's 16 rows x (head + the wave's two groups) read by four adjacent
+  // lanes per row and staged in the wave's own LDS rows (as k_tok_q4k does).
+  // Rows start on a group pair (row_stride a multiple of 128: the MoE down
+  // rows of 1408 columns start every second one half way into a super-block),
+  // so a wave's two groups lie in one super-block, at a row-dependent position
+  // that repeats every 16 rows (16 rows are whole super-blocks)
+  unsigned char *wst = lds + RED_BYTES + (size_t)wid * 16 * WROW;
+  const int64_t e_st = base + (int64_t)(rt0 * 16 + (lane >> 2)) * a.row_stride + (int64_t)g0 * 64;
+  const uint8_t *w_tile0 = a.W + (e_st >> 8) * 144;
+  const int q_st = 16 + 32 * (int)((e_st >> 6) & 3) + 16 * (lane & 3);
+  // which half of its super-block row n's groups are in (the scales' byte positions)
+  const int hq_n = (int)((((int64_t)n * a.row_stride + (int64_t)g0 * 64 + base) >> 7) & 1);
+  auto load_raw = [&](int rt, bool live, u32x4 &QR, uint32_t &HR) {
+    // rows past the end read the tensor's first super-block
+    const bool ok = live && ng > 0 && rt * 16 + (lane >> 2) < a.rows;
+    const uint8_t *sb = ok ? w_tile0 + (int64_t)(rt - rt0) * w_step : a.W;
+    QR = *(const u32x4 *)(sb + (ok ? q_st : 16));
+    HR = *(const uint32_t *)(sb + 4 * (lane & 3));
+  };
+  auto stage = [&](const u32x4 &QR, uint32_t HR, u32x2a4 (&Q)[GPW], u32x4 (&H)[NH]) {
+    unsigned char *wr = wst + (lane >> 2) * WROW;
+    *(u32x4 *)(wr + 16 + 16 * (lane & 3)) = QR;
+    *(uint32_t *)(wr + 4 * (lane & 3)) = HR;
+    const unsigned char *rd = wst + n * WROW;
+    H[0] = *(const u32x4 *)rd;
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi) Q[gi] = *(const u32x2a4 *)(rd + 16 + 32 * gi + 8 * j);
+  };
+
+  for (int pass = 0;; ++pass) {
+    if (pass > 0) __syncthreads();  // every wave is done with the previous pass's LDS
+    const int total = scan(pass);
+    const int cnt = min(16, total - 16 * pass);
+    if (cnt <= 0) return;
+    if (zero_rows) {
+      const int r0 = rt0 * 16, nr = min(a.rows, rt1 * 16) - r0;
+      for (int i = tid; i < cnt * nr; i += WPB * 64) {
+        const int t = i / nr, r = r0 + i % nr;
+        a.y[(int64_t)pl[t] * a.y_stride + r] = 0.f;
+      }
+      continue;
+    }
+    // the pair of the outputs this lane stores (component wid of its four, waves 0..3)
+    const int pj = pl[4 * j + (wid & 3)];
+
+    // x of the 16 pair slots x the wave's 128 columns, adjacent lanes on adjacent
+    // 16-byte pieces (lane l: piece l % 32 of slot 2q + l / 32); empty slots read
+    // the first pair's token (never stored), groups past the slice group 0
+    u32x4a4 xg[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int slot = 2 * q + (lane >> 5), c = lane & 31, gi = c >> 4;
+      const float *src = a.x + (int64_t)tl[slot] * a.x_stride + (int64_t)(gi < ng ? g0 + gi : 0) * 64 + 4 * (c & 15);
+      xg[q] = *(const u32x4a4 *)src;
+    }
+    u32x2a4 QA[GPW], QB[GPW];
+    u32x4 HA[NH], HB[NH];
+    int GA[GPW], GB[GPW];
+    u32x4 QRA, QRB;
+    uint32_t HRA, HRB;
+    // the first tile's weight loads go out behind the x loads
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (AL)
+      load_raw(rt0, true, QRA, HRA);
+    else
+      load_w(rt0, true, QA, HA, GA);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // back from LDS in the MFMA layout: lane (j, n) takes slot n, columns
+    // 64 gi + 32 h + 8 j .. +8 of the slice
+    u32x4a4 xr[GPW][2][2];
+    float *xst = (float *)lds + wid * 16 * XROW;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) *(u32x4 *)(xst + (2 * q + (lane >> 5)) * XROW + 4 * (lane & 31)) = xg[q];
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) xr[gi][h][u] = *(const u32x4 *)(xst + n * XROW + 64 * gi + 32 * h + 8 * j + 4 * u);
+    __syncthreads();  // every wave has its x: the LDS now holds the partial tiles
+
+    // the sum of x over sub-block j for slot n (the fp32 MFMA's A operand)
+    float ps[2 * GPW];
+#pragma unroll
+    for (int gi = 0; gi < GPW; ++gi)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float t = __uint_as_float(xr[gi][h][0].x);
+        t += __uint_as_float(xr[gi][h][0].y);
+        t += __uint_as_float(xr[gi][h][0].z);
+        t += __uint_as_float(xr[gi][h][0].w);
+        t += __uint_as_float(xr[gi][h][1].x);
+        t += __uint_as_float(xr[gi][h][1].y);
+        t += __uint_as_float(xr[gi][h][1].z);
+        t += __uint_as_float(xr[gi][h][1].w);
+        ps[2 * gi + h] = t;
+      }
+    const float t02 = tstep<32>(ps[0], ps[2], lane), t13 = tstep<32>(ps[1], ps[3], lane);
+    float xsT = tstep<16>(t02, t13, lane);
+    const bool bad = !__builtin_isfinite(xsT);
+    bf16x8 A[GPW][2][3];
+    auto split_all = [&](auto guard) {
+#pragma unroll
+      for (int gi = 0; gi < GPW; ++gi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float v[8];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            v[4 * u] = __uint_as_float(xr[gi][h][u].x);
+            v[4 * u + 1] = __uint_as_float(xr[gi][h][u].y);
+            v[4 * u + 2] = __uint_as_float(xr[gi][h][u].z);
+            v[4 * u + 3] = __uint_as_float(xr[gi][h][u].w);
+          }
+          split3<decltype(guard)::value>(v, A[gi][h][0], A[gi][h][1], A[gi][h][2]);
+        }
+    };
+    if (__builtin_amdgcn_ballot_w64(bad) != 0)
+      split_all(std::true_type());
+    else
+      split_all(std::false_type());
+    if ((j >> 1) >= ng) xsT = 0.f;  // a group past the slice
+    // sum(128 x) of each sub-block by the tiles' MFMAs (the all-8 operand)
+    f32x4 S8[GPW][2];
+    {
+      bf16x8 b128;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) b128[i] = (__bf16)128.0f;
+#pragma unroll
+      for (int gi = 0; gi < GPW; ++gi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          S8[gi][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int p = 0; p < 3; ++p)
+            S8[gi][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[gi][h][p], b128, S8[gi][h], 0, 0, 0);
+        }
+    }
+
+    int buf = 0;
+    // mid() runs between the partial tile's LDS store and the barrier
+    auto tile = [&](int rt, const u32x2a4 (&Q)[GPW], const u32x4 (&H)[NH], const int (&gs)[GPW], auto &&mid) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (ng > 0) {  // wave-uniform
+        float d1[2 * GPW], cj;
+        if constexpr (AL) {
+          const float dq = h2f(H[0].x & 0xFFFFu) * 0.0625f, dmin = h2f(H[0].x >> 16);
+          uint32_t scq, mq;
+          scale_min_quad_sel(H[0], hq_n, scq, mq);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) d1[s] = dq * ubyte(scq, s);
+          const float scj = (float)((scq >> (8 * j)) & 0xFFu), mj = (float)((mq >> (8 * j)) & 0xFFu);
+          cj = __builtin_fmaf(128.f, dq * scj, -(dmin * mj));
+        } else {
+          float cc[GPW][2];
+#pragma unroll
+          for (int gi = 0; gi < GPW; ++gi) {
+            uint32_t scp, mp;
+            scale_min_pair(H[gi], gs[gi], scp, mp);
+            const float dq = h2f(H[gi].x & 0xFFFFu) * 0.0625f, dmin = h2f(H[gi].x >> 16);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              d1[2 * gi + h] = dq * ubyte(scp, h);
+              cc[gi][h] = __builtin_fmaf(128.f, d1[2 * gi + h], -(dmin * ubyte(mp, h)));
+            }
+          }
+          const float c0 = (j & 1) ? cc[0][1] : cc[0][0], c1 = (j & 1) ? cc[1][1] : cc[1][0];
+          // a group past the slice has the tensor's first head: no coefficient
+          cj = (j >> 1) >= ng ? 0.f : ((j >> 1) ? c1 : c0);
+        }
+        f32x4 P[GPW][2];
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi) {
+          if (gi < ng) {  // wave-uniform
+            const uint32_t w0 = Q[gi].x, w1 = Q[gi].y;
+            const bf16x8 bl = codes_bf16_16q(opaque(w0 & 0x0F0F0F0Fu), opaque(w1 & 0x0F0F0F0Fu));
+            const bf16x8 bh = codes_bf16_16q(opaque((w0 >> 4) & 0x0F0F0F0Fu), opaque((w1 >> 4) & 0x0F0F0F0Fu));
+            P[gi][0] = P[gi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+              P[gi][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[gi][0][p], bl, P[gi][0], 0, 0, 0);
+              P[gi][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[gi][1][p], bh, P[gi][1], 0, 0, 0);
+            }
+          }
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xsT, cj, acc, 0, 0, 0);
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi)
+          if (gi < ng)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              acc[i] = __builtin_fmaf(d1[2 * gi], P[gi][0][i] - S8[gi][0][i], acc[i]);
+              acc[i] = __builtin_fmaf(d1[2 * gi + 1], P[gi][1][i] - S8[gi][1][i], acc[i]);
+            }
+      }
+      // the 16 column slices summed in wave order (deterministic): wave c < 4
+      // takes component c of every lane's four outputs
+      red[buf][wid][lane] = acc;
+      mid();
+      __syncthreads();
+      if (wid < 4) {
+        const float *rp = (const float *)&red[buf][0][lane] + wid;
+        float s = rp[0];
+#pragma unroll
+        for (int w = 1; w < WPB; ++w) s += rp[w * 64 * 4];
+        const int r = rt * 16 + n;
+        if (pj >= 0 && r < a.rows) a.y[(int64_t)pj * a.y_stride + r] = s;
+      }
+      buf ^= 1;
+    };
+
+    if constexpr (AL) {
+      // tile t+1's weights load while tile t multiplies, and are staged between
+      // tile t's partial store and its barrier
+      stage(QRA, HRA, QA, HA);
+      for (int rt = rt0; rt < rt1; rt += 2) {
+        load_raw(rt + 1, rt + 1 < rt1, QRB, HRB);
+        __builtin_amdgcn_sched_barrier(0);
+        tile(rt, QA, HA, GA, [&] { stage(QRB, HRB, QA, HA); });
+        __builtin_amdgcn_sched_barrier(0);
+        load_raw(rt + 2, rt + 2 < rt1, QRA, HRA);
+        __builtin_amdgcn_sched_barrier(0);
+        if (rt + 1 < rt1) tile(rt + 1, QA, HA, GA, [&] { stage(QRA, HRA, QA, HA); });
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      // two row tiles in flight: tile t+1 loads while tile t multiplies
+      for (int rt = rt0; rt < rt1; rt += 2) {
+        load_w(rt + 1, rt + 1 < rt1, QB, HB, GB);
+        __builtin_amdgcn_sched_barrier(0);
+        tile(rt, QA, HA, GA, [] {});
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(rt + 2, rt + 2 < rt1, QA, HA, GA);
+        __builtin_amdgcn_sched_barrier(0);
+        if (rt + 1 < rt1) tile(rt + 1, QB, HB, GB, [] {});
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+}
+
+// True when the 16-pair tiles take a grouped launch: Q4_K rows of at most 2048
+// columns in 64-column groups; the gate+up launch's gate and up halves adjacent.
+static bool grp_tok_ok(bool gate_up, const MoeGrpArgs &a) {
+  if (a.dim1 <= 0 || a.dim1 > GT_WPB * TOK_GPW * 64 || a.dim1 % 64 != 0) return false;
+  if (a.base0 % 64 != 0 || a.row_stride % 64 != 0 || a.expert_stride % 64 != 0) return false;
+  if (gate_up && (a.gu == nullptr || a.base1 != a.base0 + (int64_t)a.rows * a.row_stride)) return false;
+  return a.S >= 1 && a.rows >= 1 && a.x_div >= 1 && a.n_experts >= 1;
+}
+
 bool moe_grp_ok(int type, const MoeGrpArgs &a) {
   if (type != T_Q4_K) return false;
   if (a.dim1 <= 0 || a.dim1 % 128 != 0 || a.dim1 > MG_MAX_DIM1) return false;
@@ -978,8 +1321,31 @@ hipError_t moe_grp_init_device() {
 }
 
 hipError_t launch_moe_grp(int type, bool gate_up, const MoeGrpArgs &a, const DevInfo &dev, hipStream_t s) {
-  (void)dev;
   if (!moe_grp_ok(type, a)) return hipErrorNotSupported;
+  if (grp_tok_ok(gate_up, a)) {
+    // 16-pair tiles: the gate+up launch writes the gate and up rows (2 rows per
+    // pair) and k_gelu_mul forms h; row blocks per expert so that the experts'
+    // workgroups about fill the CUs
+    MoeGrpArgs b = a;
+    if (gate_up) {
+      b.rows = 2 * a.rows;
+      b.y = a.gu;
+      b.y_stride = 2 * (int64_t)a.rows;
+    }
+    const int n_rt = (b.rows + 15) / 16;
+    const int gx = std::max(1, std::min(n_rt, GT_GX_PER_CU * dev.cu_count / std::max(1, b.n_experts)));
+    const dim3 grid((unsigned)gx, (unsigned)b.n_experts + 1);
+    // rows starting on a group pair and whole 128-column slices: the coalesced,
+    // LDS-staged weight tiles
+    const bool al = b.base0 % 128 == 0 && b.row_stride % 128 == 0 && b.expert_stride % 128 == 0 && b.dim1 % 128 == 0;
+    if (al)
+      hipLaunchKernelGGL(k_grp_q4k<true>, grid, dim3(GT_WPB * 64), 0, s, b);
+    else
+      hipLaunchKernelGGL(k_grp_q4k<false>, grid, dim3(GT_WPB * 64), 0, s, b);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !gate_up) return e;
+    return launch_gelu_mul(a.gu, a.rows, a.S, a.y, a.y_stride, s);
+  }
   const int ur = gate_up ? 16 : 32;
   const int units = (a.rows + ur - 1) / ur;
   const dim3 grid((unsigned)((units + MG_UPW * MG_WPB - 1) / (MG_UPW * MG_WPB)), (unsigned)a.n_experts + 1);

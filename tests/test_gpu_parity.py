@@ -661,11 +661,12 @@ def test_moe_batch_equals_tokens_alone(g4, ctx, oracle, fmt):
     assert_dots(Yb.reshape(-1), y64.reshape(-1), bound.reshape(-1), "moe batch")
 
 
-@pytest.mark.parametrize("fmt,T,K,D", [(Q4_K, 16, 8, 512), (Q4_K, 5, 3, 512), (Q4_K, 39, 8, 512),
+@pytest.mark.parametrize("fmt,T,K,D", [(Q4_K, 16, 8, 512), (Q4_K, 5, 3, 512), (Q4_K, 32, 8, 512),
                                        (Q4_K, 7, 1, 100), (Q4_0, 24, 8, 256), (Q8_0, 33, 6, 192),
                                        (Q5_K, 9, 8, 128)])
 def test_moe_fused_down_tokens(g4, ctx, oracle, fmt, T, K, D):
-    """Down rows of 17..24 chunks (ff = 1408 here) for 2..39 tokens: one launch
+    """Down rows of 17..24 chunks (ff = 1408 here) for 2..32 Q4_K tokens (more run
+    the experts grouped) and any count of the other formats: one launch
     does the down projection and the weighted sum, workgroup (row block, token)
     with one wave per slot and several 8-row steps per wave (partial last blocks,
     idle slot waves for k < 8, rows that end inside a step at D = 100).  Within
@@ -708,11 +709,12 @@ def test_moe_fused_down_tokens(g4, ctx, oracle, fmt, T, K, D):
 
 
 @pytest.mark.parametrize("fmt,T,K,D,E,case", [(Q4_K, 16, 8, 2048, 32, ""), (Q4_K, 2, 1, 1088, 16, ""),
-                                              (Q4_K, 39, 3, 2048, 16, ""), (Q8_0, 5, 8, 1088, 8, ""),
+                                              (Q4_K, 32, 3, 2048, 16, ""), (Q8_0, 5, 8, 1088, 8, ""),
                                               (Q4_0, 16, 8, 2048, 256, ""), (Q5_K, 7, 6, 1536, 16, ""),
                                               (Q6_K, 3, 8, 2048, 16, ""), (Q4_K, 6, 4, 2048, 16, "nan")])
 def test_moe_gate_up_slot_waves(g4, ctx, oracle, fmt, T, K, D, E, case):
-    """Gate+up of 2 or more tokens with rows of 17..32 chunks: workgroup (row
+    """Gate+up of 2 or more tokens (up to 32 of Q4_K, where more run the experts
+    grouped) with rows of 17..32 chunks: workgroup (row
     block, token), one wave per slot, routing once per workgroup in 512 threads
     (up to 256 experts; "nan": a NaN logit, the reference's scans).  The routing
     equals the oracle's exactly, the output is within the oracle's bound, equal
@@ -743,13 +745,13 @@ def test_moe_gate_up_slot_waves(g4, ctx, oracle, fmt, T, K, D, E, case):
 
 @pytest.mark.parametrize("case", ["t64", "t80_e8", "ff384", "nonfinite", "ref_gates"])
 def test_moe_grouped_by_expert(g4, ctx, oracle, case):
-    """Calls of 40 or more Q4_K tokens run each expert once for all of its (token,
+    """Calls of 33 or more Q4_K tokens run each expert once for all of its (token,
     slot) pairs on the matrix cores (3 x bf16 products, fp32 sums).  The routed
     and the id-taking entry points give the same bits; every output is within the
     bound; a token alone (row kernels) rounds differently but shares the bound.
     t80_e8: ten pairs per expert on average, so experts take two or more passes
-    of eight pairs; ff384: down rows of 384 columns, every second one starting half
-    way into a super-block; nonfinite: +inf, NaN and -inf activations reach only
+    of sixteen pairs; ff384: down rows of 384 columns, every second one starting half
+    way into a super-block (staged at its group pair); nonfinite: +inf, NaN and -inf activations reach only
     their own tokens; ref_gates: un-renormalised gates times a per-expert down
     scale (Llama.kt:300-337)."""
     announce("moe grouped %s" % case)
@@ -822,12 +824,13 @@ def test_moe_routed_dev_calls(g4, ctx, oracle):
 
 @pytest.mark.parametrize("case", ["one_expert", "widest_rows", "ragged_rows", "k8_e256"])
 def test_moe_grouped_edges(g4, ctx, oracle, case):
-    """Edges of the expert-grouped calls (40+ tokens) with the ids given:
-    one_expert: all 256 pairs on one expert (32 passes of eight pairs, the other
-    experts idle); widest_rows: 3072 columns (the largest LDS operand set, 150 KB);
-    ragged_rows: workgroups left with fewer units than they hold waves for (40
-    gate+up units and 12 down units against 16 per workgroup), down rows of 640
-    columns (2.5 super-blocks); k8_e256: 256 experts, eight slots per token."""
+    """Edges of the expert-grouped calls (33+ tokens) with the ids given:
+    one_expert: all 256 pairs on one expert (16 passes of sixteen pairs, the other
+    experts idle); widest_rows: 3072 columns, past the 16-pair tiles' 2048, so the
+    eight-pair kernel (its largest LDS operand set, 150 KB); ragged_rows: rows of
+    384 and 640 columns (3 and 5 of the 16 waves hold columns), down rows of 640
+    columns (2.5 super-blocks, every second one staged from half way into one);
+    k8_e256: 256 experts, eight slots per token."""
     announce("moe grouped edge %s" % case)
     E, D, FF, K, T = 16, 512, 256, 4, 64
     if case == "widest_rows":
@@ -892,15 +895,15 @@ def test_moe_dev_out_of_range_ids(g4, ctx, oracle, tokens):
 def test_moe_repeated_calls(g4, ctx, oracle):
     """Back-to-back MoE calls on one context with changing token counts: the
     context's scratch is re-carved per call and nothing leaks from one call to the next.
-    40 tokens run the experts grouped; 33 and 39 take the per-pair launches with
-    pair counts (132, 156) that do not divide the resident workgroups."""
+    33 and 40 tokens run the experts grouped; 25 and 31 take the per-pair launches
+    with pair counts (100, 124) that do not divide the resident workgroups."""
     announce("moe repeated calls")
     E, D, FF, K = 16, 512, 256, 4
     gu = synth.q4_k(48, "gu", E * 2 * FF * D)
     dn = synth.q4_k(48, "dn", E * D * FF)
     wgu = upload(g4, ctx, Q4_K, gu, E * 2 * FF * D)
     wdn = upload(g4, ctx, Q4_K, dn, E * D * FF)
-    for call, T in enumerate([3, 16, 1, 16, 40, 2, 33, 39]):
+    for call, T in enumerate([3, 16, 1, 16, 40, 2, 31, 25, 33]):
         lg = synth.activations(48, "lg%d" % call, T * E).reshape(T, E)
         X = synth.activations(48, "X%d" % call, T * D).reshape(T, D)
         ids, gw = g4.moe_route(ctx, lg, K, True)
