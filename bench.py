@@ -59,7 +59,7 @@ TRAFFIC_BYTES = {
     "q4_k_batched_8192x2048_m64": 15843968,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t1": 40018112,
     "moe_q4_k_128x(2816x2048+2048x1408)_top8_t16": 479384304,
-    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t128": 987322060,
+    "moe_q4_k_128x(2816x2048+2048x1408)_top8_t128": 727389920,
     "q5_k_matvec_8192x2048": 11777024,
     "q6_k_matvec_8192x2048": 14138240,
     "q4_0_ffn_block_decode_token": 29151872,
@@ -314,12 +314,13 @@ class MoeQ4_K(Workload):
         import synth
         self.T = tokens
         self.name = "moe_q4_k_128x(2816x2048+2048x1408)_top8_t%d" % tokens
-        # up to 39 tokens: the down projection and the weighted sum share a launch
-        # (one row step per wave for one token, looped row steps for more); 40 or
+        # up to 32 tokens: the down projection and the weighted sum share a launch
+        # (one row step per wave for one token, looped row steps for more); 33 or
         # more tokens: a routing launch, then the experts grouped on the matrix cores
-        if tokens >= 40:
-            self.dominant_name = ("g4_moe_routed: k_route + k_moe_grp<true> (gate+up) + k_moe_grp<false> (down) (experts grouped "
-                                  "on the matrix cores) + k_moe_combine")
+        # (16-pair tiles: gate and up rows, gelu, down), then the weighted sum
+        if tokens >= 33:
+            self.dominant_name = ("g4_moe_routed: k_route + k_grp_q4k<true> (gate+up rows) + k_gelu_mul4 + "
+                                  "k_grp_q4k<true> (down) (experts grouped on the matrix cores) + k_moe_combine")
         else:
             self.dominant_name = ("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE> (routing + gate_up) + " +
                                   ("k_moe_down_xl<FmtQ4_K> (down + weighted sum)" if tokens == 1 else

@@ -52,7 +52,8 @@ def test_noalloc_matches_the_allocating_entry_point(g4, ctx, experts, with_scale
     ex = experts
     scale = (torch.from_numpy(np.abs(synth.activations(58, "sc", ex["E"])) + 0.5).cuda() if with_scale else None)
     # each call smaller than the one before; 48 tokens run the experts grouped
-    # (k_route, k_moe_grp) with their intermediates in the fixed scratch
+    # (k_route, the 16-pair tiles, k_gelu_mul) with their intermediates in the
+    # fixed scratch
     for T, seed in ((48, 5), (16, 1), (3, 2)):
         announce("noalloc moe T=%d scale=%s" % (T, with_scale))
         X, lg, ((i0, w0, y0), (i1, w1, y1)) = _bufs(ex, T, seed + (10 if with_scale else 0))
