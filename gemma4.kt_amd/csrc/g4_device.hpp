@@ -326,6 +326,32 @@ struct FmtQ4_K {
   G4_DEV static float k_subblocks(float d1, float lo, float m1, float s0, float d2, float hi, float m2, float s1) {
     return (rounded(d1 * lo) - rounded(m1 * s0)) + (rounded(d2 * hi) - rounded(m2 * s1));
   }
+  // getScaleMinK4 for group g without a branch: the scale bytes of sub-blocks
+  // 2g, 2g+1 are ((w >> sh) & mA) | ((y >> shk) & mB), the mins the same of
+  // (w >> sh4) and z, with (y, z, w) the three scale dwords.  g < 2: mA = 0,
+  // mB = 0x3F3F, shk = sh; g >= 2: the low nibbles from w, bits 6..7 of y and z
+  // on top (mA = 0x0F0F, mB = 0x3030, shk = sh + 2).  For callers whose lanes
+  // keep one g over all their rows, so the selector is formed once.
+  struct Sel {
+    uint32_t sh, shk, sh4, mA, mB;
+  };
+  G4_DEV static Sel select(int g) {
+    const uint32_t sh = (uint32_t)(g & 1) * 16u;
+    const bool h = g >= 2;
+    return Sel{sh, sh + (h ? 2u : 0u), sh + 4u, h ? 0x0F0Fu : 0u, h ? 0x3030u : 0x3F3Fu};
+  }
+  // dot() for the group that q selects, the same arithmetic in the same order
+  G4_DEV static float dot_sel(const uint32_t (&D)[NDW], const float *x, const float *s, const Sel &q) {
+    float lo = 0.f, hi = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) nib4_fma2(D[i], x + 4 * i, x + 32 + 4 * i, lo, hi);
+    const uint32_t scp = opaque(((D[11] >> q.sh) & q.mA) | ((D[9] >> q.shk) & q.mB));
+    const uint32_t mp = opaque(((D[11] >> q.sh4) & q.mA) | ((D[10] >> q.shk) & q.mB));
+    const float d = h2f(D[8] & 0xFFFFu) * 0x1p24f, dmin = h2f(D[8] >> 16);
+    const float d1 = d * ubyte(scp, 0), d2 = d * ubyte(scp, 1) * 0.0625f;
+    const float m1 = dmin * ubyte(mp, 0), m2 = dmin * ubyte(mp, 1);
+    return k_subblocks(d1, lo, m1, s[0], d2, hi, m2, s[1]);
+  }
 };
 
 // Q5_K: super-block {fp16 d, fp16 dmin, scales[12], qh[32], qs[128]} (176 B,

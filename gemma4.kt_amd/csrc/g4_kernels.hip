@@ -302,7 +302,7 @@ G4_DEV void route_token(const float *lg, int E, int K, int renorm, const float *
 // --------------------------------------------------------------- engine ----
 
 template <class F, int LPR, int CPL, int EPI, bool MULTI, bool NORM, bool ROUTE = false, bool XL = false, int WPB = 4,
-          bool SLOTW = false>
+          bool SLOTW = false, bool KSEL = false>
 __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
   constexpr int NT = 64 * WPB;                   // threads per workgroup (WPB waves)
   constexpr int RT = F::RT / CPL > 0 ? F::RT / CPL : 1;  // row steps per tile (about F::RT chunk loads per lane)
@@ -331,6 +331,10 @@ __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
   // token run side by side (with a grid x extent that is a multiple of 8, on one
   // XCD), so tokens that share an expert read its rows through one L2
   static_assert(!SLOTW || (EPI == EPI_GELU_PAIR && !MULTI && !NORM && !XL && WPB == 8), "slot per wave: gate+up");
+  // KSEL (Q4_K with every base and stride on whole super-blocks): chunk c of
+  // any row is group c & 3 of its super-block, and every chunk a lane takes has
+  // c = q (mod 4), so the lane's scale selector is formed once
+  static_assert(!KSEL || (F::TYPE == T_Q4_K && LPR % 4 == 0), "KSEL: Q4_K rows");
   constexpr int NSX = F::NS > 0 ? F::NS : 1;
   // x layout in LDS (16-byte slots): chunk ch's segment i sits at slot
   // ch * 16 + (i ^ (ch & 15)) -- the 8 lanes one LDS cycle serves read 8
@@ -346,6 +350,7 @@ __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: tile loop control stays scalar
   constexpr int wpb = WPB;
   const int gi = lane / LPR, q = lane % LPR;
+  const FmtQ4_K::Sel ksel = FmtQ4_K::select(q & 3);  // KSEL
   const int seg = blockIdx.y;
   const int C = a.dim1 >> 6;
   const float *x = a.x + (int64_t)(SLOTW ? seg : seg / a.x_div) * a.x_stride;
@@ -499,10 +504,13 @@ __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
           read_x(ch, xu);
 #pragma unroll
           for (int j = 0; j < NSX; ++j) su[j] = xsl[ch][j];
-          r = F::dot(D[k][u], xu, su, E[k][u]);
+          if constexpr (KSEL) r = FmtQ4_K::dot_sel(D[k][u], xu, su, ksel);
+          else r = F::dot(D[k][u], xu, su, E[k][u]);
           // one chunk's x in VGPRs at a time: this chunk's dot is done before
           // the next chunk's LDS reads are issued
           asm volatile("" : "+v"(r)::"memory");
+        } else if constexpr (KSEL) {
+          r = FmtQ4_K::dot_sel(D[k][u], xv[u], xs[u], ksel);
         } else {
           r = F::dot(D[k][u], xv[u], xs[u], E[k][u]);
         }
@@ -999,9 +1007,15 @@ __global__ __launch_bounds__(512) void k_moe_down_xl(RowsArgs a, const float *gw
 // rows through the same L2.  Every dot has the bits of the per-pair XL launch
 // and the k row values are summed in slot order as k_moe_combine does.
 constexpr int MOE_DOWN_T_MAX_ROWS = 512;  // rows per workgroup (nrt <= 64)
-
-template <class F>
+//
+// STEP (Q4_K only; row strides of whole super-blocks per 8 rows, expert bases on
+// super-blocks, experts under 2 GiB): a lane's chunks keep their group g on
+// every row step, so each chunk's super-block offset advances by one uniform
+// byte count from a wave-uniform expert base and its scale selector
+// (FmtQ4_K::select) is formed once.
+template <class F, bool STEP>
 __global__ __launch_bounds__(512) void k_moe_down_xlt(RowsArgs a, const float *gw, int32_t K, int32_t nrt) {
+  static_assert(!STEP || F::TYPE == T_Q4_K, "STEP takes the Q4_K layout");
   constexpr int NT = 512, LPR = 8, CPL = 3, NCH = LPR * CPL, RPW = 64 / LPR, NDW = F::NDW;
   constexpr int NSX = F::NS > 0 ? F::NS : 1;
   constexpr int XS = NCH * 16;                    // 16-byte x segments of one slot
@@ -1030,14 +1044,39 @@ __global__ __launch_bounds__(512) void k_moe_down_xlt(RowsArgs a, const float *g
   const int expert = a.ids[tok * K + (wid < K ? wid : 0)];
   const bool bad = (wid >= K) | (expert < 0) | (expert >= a.expert_count);
   const int64_t ebase = bad ? 0 : (int64_t)expert * a.expert_stride;
+  const uint8_t *wb = a.W0 + ((a.base0 + ebase) >> 8) * 144;  // STEP: the expert's first super-block
+  const uint32_t step = (uint32_t)(a.row_stride >> 5) * 144u;   // STEP: bytes per 8 rows
+  uint32_t off0[CPL], qo[CPL];
+  FmtQ4_K::Sel sel[CPL];
+  if constexpr (STEP) {
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+      const int64_t e0 = (int64_t)(row0 + gi) * a.row_stride + (int64_t)(u * LPR + q) * 64;
+      const int g = (int)((e0 >> 6) & 3);
+      off0[u] = (uint32_t)((e0 >> 8) * 144);
+      qo[u] = 16u + 32u * (uint32_t)g;
+      sel[u] = FmtQ4_K::select(g);
+    }
+  }
   auto load = [&](int t, uint32_t (&D)[CPL][NDW], bool (&ok)[CPL], int64_t (&E)[CPL]) {
     const int lr = row0 + t * RPW + gi;
 #pragma unroll
     for (int u = 0; u < CPL; ++u) {
       const int c = u * LPR + q;
       ok[u] = !bad && t < nrt && c < C && lr < a.rows;
-      E[u] = a.base0 + ebase + (int64_t)lr * a.row_stride + (int64_t)c * 64;
-      F::load(a.W0, ok[u] ? E[u] : 0, D[u]);
+      if constexpr (STEP) {
+        // a masked chunk reads the expert's first super-block
+        const uint32_t o = ok[u] ? off0[u] + (uint32_t)t * step : 0u;
+        const u32x4 h = *(const u32x4 *)(wb + o);
+        const u32x4 *qs = (const u32x4 *)(wb + (o + qo[u]));
+        const u32x4 q0 = qs[0], q1 = qs[1];
+        D[u][0] = q0.x; D[u][1] = q0.y; D[u][2] = q0.z; D[u][3] = q0.w;
+        D[u][4] = q1.x; D[u][5] = q1.y; D[u][6] = q1.z; D[u][7] = q1.w;
+        D[u][8] = h.x; D[u][9] = h.y; D[u][10] = h.z; D[u][11] = h.w;
+      } else {
+        E[u] = a.base0 + ebase + (int64_t)lr * a.row_stride + (int64_t)c * 64;
+        F::load(a.W0, ok[u] ? E[u] : 0, D[u]);
+      }
     }
   };
   uint32_t DA[CPL][NDW], DB[CPL][NDW];
@@ -1081,7 +1120,9 @@ __global__ __launch_bounds__(512) void k_moe_down_xlt(RowsArgs a, const float *g
       read_x(wid, ch, xu);
 #pragma unroll
       for (int i = 0; i < NSX; ++i) su[i] = xsl[wid][ch][i];
-      float r = F::dot(D[u], xu, su, E[u]);
+      float r;
+      if constexpr (STEP) r = FmtQ4_K::dot_sel(D[u], xu, su, sel[u]);
+      else r = F::dot(D[u], xu, su, E[u]);
       // one chunk's x in VGPRs at a time
       asm volatile("" : "+v"(r)::"memory");
       acc += ok[u] ? r : 0.f;
@@ -1254,6 +1295,12 @@ bool rows_norm_ok(int type, const RowsArgs &a, bool paired) {
 
 int max_argmax_blocks(const DevInfo &dev) { return dev.cu_count * 8; }
 
+// Q4_K rows whose chunks sit on fixed super-block groups (the KSEL kernels):
+// every base and stride a whole number of 256-element super-blocks.
+static bool q4k_groups_fixed(const RowsArgs &a) {
+  return a.base0 % 256 == 0 && a.base1 % 256 == 0 && a.row_stride % 256 == 0 && a.expert_stride % 256 == 0;
+}
+
 // A format's tiles with one row step (F::RT = 1): more, smaller tiles.
 template <class F>
 struct OneStep : F {
@@ -1298,6 +1345,24 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
       else k = norm ? k_rows<F, LPR, 1, EPI_GELU_PAIR, false, true> : k_rows<F, LPR, 1, EPI_GELU_PAIR, false, false>;
     }
   }
+  // Q4_K matvecs and gate+up launches (single pass, no fused norm) with each
+  // lane's scale selector formed once (the same results)
+  bool ksel = false;
+  if constexpr (F::TYPE == T_Q4_K && LPR % 4 == 0 && !XL) {
+    if (k && q4k_groups_fixed(a) && !multi && !norm) {
+      if (epi == EPI_STORE) {
+        k = k_rows<F, LPR, CPL, EPI_STORE, false, false, false, false, WPB, false, true>;
+        ksel = true;
+      }
+      if constexpr (WPB == 4 && CPL == 1 && F::RT >= 2) {
+        if (epi == EPI_GELU_PAIR) {
+          k = route ? k_rows<F, LPR, 1, EPI_GELU_PAIR, false, false, true, false, 4, false, true>
+                    : k_rows<F, LPR, 1, EPI_GELU_PAIR, false, false, false, false, 4, false, true>;
+          ksel = true;
+        }
+      }
+    }
+  }
   if (!k) return hipErrorInvalidValue;
   if (multi && !(LPR == 64 && CPL == 2)) return hipErrorInvalidValue;
 
@@ -1305,8 +1370,8 @@ static hipError_t launch_fast_cfg(int epi, const RowsArgs &a, int segments, cons
   // the launch fills exactly that many waves when there are tiles enough.
   // Looked up once per kernel; contexts on other threads may race to store the
   // same value, hence relaxed atomics.
-  static std::atomic<int> resident[3][2][2][2];
-  std::atomic<int> &slot = resident[epi][multi ? 1 : 0][norm ? 1 : 0][route ? 1 : 0];
+  static std::atomic<int> resident[3][2][2][2][2];
+  std::atomic<int> &slot = resident[epi][multi ? 1 : 0][norm ? 1 : 0][route ? 1 : 0][ksel ? 1 : 0];
   int res = slot.load(std::memory_order_relaxed);
   if (res == 0) {
     int nb = 0;
@@ -1580,7 +1645,14 @@ static hipError_t launch_moe_down_cfg(const RowsArgs &a, const float *gw, int32_
       if (nrt < 1) nrt = 1;
       if (nrt * 8 <= MOE_DOWN_T_MAX_ROWS) {
         const int64_t nb = (steps + nrt - 1) / nrt;
-        hipLaunchKernelGGL(k_moe_down_xlt<F>, dim3((unsigned)nb, T), dim3(512), 0, s, a, gw, K, (int32_t)nrt);
+        if constexpr (F::TYPE == T_Q4_K) {
+          if (a.row_stride % 32 == 0 && a.base0 % 256 == 0 && a.expert_stride % 256 == 0 &&
+              (int64_t)a.rows * a.row_stride / 256 * 144 + 256 < (1ll << 31)) {
+            hipLaunchKernelGGL((k_moe_down_xlt<F, true>), dim3((unsigned)nb, T), dim3(512), 0, s, a, gw, K, (int32_t)nrt);
+            return hipGetLastError();
+          }
+        }
+        hipLaunchKernelGGL((k_moe_down_xlt<F, false>), dim3((unsigned)nb, T), dim3(512), 0, s, a, gw, K, (int32_t)nrt);
         return hipGetLastError();
       }
     }
@@ -1621,6 +1693,17 @@ static hipError_t launch_moe_gate_up_t(const RowsArgs &a, int32_t T, const DevIn
   int64_t nb = dev.cu_count / T;
   if (nb > n_tiles) nb = n_tiles;
   if (nb < 1) nb = 1;
+  if constexpr (F::TYPE == T_Q4_K) {
+    if (q4k_groups_fixed(a)) {
+      if (a.route_logits)
+        hipLaunchKernelGGL((k_rows<F, 32, 1, EPI_GELU_PAIR, false, false, true, false, 8, true, true>),
+                           dim3((unsigned)nb, T), dim3(512), 0, s, a);
+      else
+        hipLaunchKernelGGL((k_rows<F, 32, 1, EPI_GELU_PAIR, false, false, false, false, 8, true, true>),
+                           dim3((unsigned)nb, T), dim3(512), 0, s, a);
+      return hipGetLastError();
+    }
+  }
   if (a.route_logits)
     hipLaunchKernelGGL((k_rows<F, 32, 1, EPI_GELU_PAIR, false, false, true, false, 8, true>), dim3((unsigned)nb, T),
                        dim3(512), 0, s, a);
