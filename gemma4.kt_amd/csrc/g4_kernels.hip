@@ -415,6 +415,16 @@ __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
 
   // `live` false: a prefetch past the wave's last tile (issued anyway so every
   // path through the loop has the same number of loads in flight).
+  // SADDR (KSEL with a slot per wave, a launch bound by vector-ALU issue): a
+  // chunk's bytes sit at a wave-uniform row address (the step's first row) plus
+  // a lane offset fixed for the launch (its row in the step, its super-block),
+  // so a tile's addresses cost scalar arithmetic and one select per chunk
+  constexpr bool SADDR = KSEL && SLOTW;
+  const int64_t rbytes = (a.row_stride >> 8) * 144;  // SADDR: bytes per row
+  uint32_t lane_off[CPL];
+#pragma unroll
+  for (int u = 0; u < CPL; ++u) lane_off[u] = (uint32_t)(gi * rbytes + ((u * LPR + q) >> 2) * 144);
+  const uint32_t q_off = 16u + 32u * (uint32_t)(q & 3);
   auto load_tile = [&](int t, int pass, bool live, uint32_t (&D)[RT][CPL][NDW], bool (&ok)[RT][CPL],
                        int64_t (&E)[RT][CPL]) {
 #pragma unroll
@@ -423,6 +433,27 @@ __global__ __launch_bounds__(64 * WPB) void k_rows(RowsArgs a) {
       const uint8_t *W;
       int64_t base;
       row_of(t, k, lr, W, base);
+      if constexpr (SADDR) {
+        // the step's first row (uniform); past the last row or tile: the matrix's first row
+        const int lr0 = lr - gi;
+        const bool in = live && lr0 < a.rows;
+        const uint8_t *wrow = W + ((base + ebase) >> 8) * 144 + (in ? (int64_t)lr0 * rbytes : 0);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) {
+          const int c = (pass * CPL + u) * LPR + q;
+          ok[k][u] = live && c < C && lr < a.rows && !bad_expert;
+          // a masked chunk reads the row's first super-block
+          const uint32_t o = ok[k][u] ? lane_off[u] : 0u;
+          const u32x4 h = *(const u32x4 *)(wrow + o);
+          const u32x4 *qs = (const u32x4 *)(wrow + (o + q_off));
+          const u32x4 q0 = qs[0], q1 = qs[1];
+          uint32_t(&Du)[NDW] = D[k][u];
+          Du[0] = q0.x; Du[1] = q0.y; Du[2] = q0.z; Du[3] = q0.w;
+          Du[4] = q1.x; Du[5] = q1.y; Du[6] = q1.z; Du[7] = q1.w;
+          Du[8] = h.x; Du[9] = h.y; Du[10] = h.z; Du[11] = h.w;
+        }
+        continue;
+      }
 #pragma unroll
       for (int u = 0; u < CPL; ++u) {
         const int c = (pass * CPL + u) * LPR + q;
