@@ -314,11 +314,11 @@ class MoeQ4_K(Workload):
         import synth
         self.T = tokens
         self.name = "moe_q4_k_128x(2816x2048+2048x1408)_top8_t%d" % tokens
-        # up to 32 tokens: the down projection and the weighted sum share a launch
-        # (one row step per wave for one token, looped row steps for more); 33 or
+        # up to 40 tokens: the down projection and the weighted sum share a launch
+        # (one row step per wave for one token, looped row steps for more); 41 or
         # more tokens: a routing launch, then the experts grouped on the matrix cores
         # (16-pair tiles: gate and up rows, gelu, down), then the weighted sum
-        if tokens >= 33:
+        if tokens >= 41:
             self.dominant_name = ("g4_moe_routed: k_route + k_grp_q4k<true> (gate+up rows) + k_gelu_mul4 + "
                                   "k_grp_q4k<true> (down) (experts grouped on the matrix cores) + k_moe_combine")
         else:

@@ -475,10 +475,10 @@ int check_moe(g4_ctx *ctx, const g4_weight *wgu, const g4_weight *wdn, int32_t T
 // the ids and weights it stores out.
 // Calls of at least this many tokens run the experts grouped (launch_moe_grp):
 // measured on the 128-expert top-8 shape (alternating runs, one box), the grouped
-// launches take 231, 233, 239 and 288 us at 33, 40, 64 and 128 tokens against
-// 261, 260, 374 and 723 us for the per-pair ones, and about 222-230 us from 16 to
-// 32 tokens, where the per-pair ones take 100-193 us.
-constexpr int32_t MOE_GROUPED_MIN_T = 33;
+// launches take 231, 233, 235, 239 and 288 us at 33, 40, 48, 64 and 128 tokens
+// against 201, 233, 275, 332 and 723 us for the per-pair ones, and about 222-230
+// us from 16 to 32 tokens, where the per-pair ones take 101-180 us.
+constexpr int32_t MOE_GROUPED_MIN_T = 41;
 
 struct MoeRoute {
   const float *d_logits;

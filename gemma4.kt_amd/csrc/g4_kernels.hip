@@ -1671,9 +1671,12 @@ static hipError_t launch_moe_down_cfg(const RowsArgs &a, const float *gw, int32_
   // about one workgroup per CU over all tokens
   if constexpr (F::NDW <= 20) {
     if (a.dim1 > 16 * 64 && a.dim1 <= 24 * 64) {
+      // at most one workgroup per CU over all tokens (one is resident per CU,
+      // and a partial second round would double the launch)
       const int64_t steps = (a.rows + 7) / 8;
-      int64_t nrt = (steps * T + dev.cu_count - 1) / dev.cu_count;
-      if (nrt < 1) nrt = 1;
+      int64_t nbm = dev.cu_count / T;
+      if (nbm < 1) nbm = 1;
+      const int64_t nrt = (steps + nbm - 1) / nbm;
       if (nrt * 8 <= MOE_DOWN_T_MAX_ROWS) {
         const int64_t nb = (steps + nrt - 1) / nrt;
         if constexpr (F::TYPE == T_Q4_K) {

@@ -172,7 +172,7 @@ int g4_moe_route_dev(g4_ctx *ctx, const float *d_logits, int32_t T, int32_t n_ex
  * (G4_ERR_OUT_OF_RANGE).  g4_moe_dev cannot (the ids are device memory): a slot
  * whose id lies outside [0, n_experts) contributes nothing (its hidden vector
  * and down rows are zero), so Y is the weighted sum over the valid slots.
- * Calls of 33 or more tokens with Q4_K weights (dim and ff multiples of 128 up
+ * Calls of 41 or more tokens with Q4_K weights (dim and ff multiples of 128 up
  * to 3072, at most 4096 (token, slot) pairs) run the experts grouped by expert
  * on the matrix cores: every dot within the same bound, but rounded differently
  * from the same tokens in smaller calls. */

@@ -561,8 +561,8 @@ def moe_slabs(g4, ctx, c):
 
 
 # the configured workload (128 experts, top-8, dim 2048, ff 1408): one token and
-# 16 tokens take the per-pair launches, 40 and 128 the expert-grouped ones
-@pytest.mark.parametrize("tokens", [1, 16, 40, 128])
+# 16 tokens take the per-pair launches, 48 and 128 the expert-grouped ones
+@pytest.mark.parametrize("tokens", [1, 16, 48, 128])
 def test_moe_q4_k(g4, ctx, oracle, tokens):
     announce("workload moe q4_k T=%d" % tokens)
     c = synth.moe_q4_k(tokens)
@@ -745,7 +745,7 @@ def test_moe_gate_up_slot_waves(g4, ctx, oracle, fmt, T, K, D, E, case):
 
 @pytest.mark.parametrize("case", ["t64", "t80_e8", "ff384", "nonfinite", "ref_gates"])
 def test_moe_grouped_by_expert(g4, ctx, oracle, case):
-    """Calls of 33 or more Q4_K tokens run each expert once for all of its (token,
+    """Calls of 41 or more Q4_K tokens run each expert once for all of its (token,
     slot) pairs on the matrix cores (3 x bf16 products, fp32 sums).  The routed
     and the id-taking entry points give the same bits; every output is within the
     bound; a token alone (row kernels) rounds differently but shares the bound.
@@ -824,7 +824,7 @@ def test_moe_routed_dev_calls(g4, ctx, oracle):
 
 @pytest.mark.parametrize("case", ["one_expert", "widest_rows", "ragged_rows", "k8_e256"])
 def test_moe_grouped_edges(g4, ctx, oracle, case):
-    """Edges of the expert-grouped calls (33+ tokens) with the ids given:
+    """Edges of the expert-grouped calls (41+ tokens) with the ids given:
     one_expert: all 256 pairs on one expert (16 passes of sixteen pairs, the other
     experts idle); widest_rows: 3072 columns, past the 16-pair tiles' 2048, so the
     eight-pair kernel (its largest LDS operand set, 150 KB); ragged_rows: rows of
@@ -895,15 +895,16 @@ def test_moe_dev_out_of_range_ids(g4, ctx, oracle, tokens):
 def test_moe_repeated_calls(g4, ctx, oracle):
     """Back-to-back MoE calls on one context with changing token counts: the
     context's scratch is re-carved per call and nothing leaks from one call to the next.
-    33 and 40 tokens run the experts grouped; 25 and 31 take the per-pair launches
-    with pair counts (100, 124) that do not divide the resident workgroups."""
+    41 and 48 tokens run the experts grouped; 25, 31 and 33 take the per-pair
+    launches with pair counts (100, 124, 132) that do not divide the resident
+    workgroups."""
     announce("moe repeated calls")
     E, D, FF, K = 16, 512, 256, 4
     gu = synth.q4_k(48, "gu", E * 2 * FF * D)
     dn = synth.q4_k(48, "dn", E * D * FF)
     wgu = upload(g4, ctx, Q4_K, gu, E * 2 * FF * D)
     wdn = upload(g4, ctx, Q4_K, dn, E * D * FF)
-    for call, T in enumerate([3, 16, 1, 16, 40, 2, 31, 25, 33]):
+    for call, T in enumerate([3, 16, 1, 16, 48, 2, 31, 25, 33, 41]):
         lg = synth.activations(48, "lg%d" % call, T * E).reshape(T, E)
         X = synth.activations(48, "X%d" % call, T * D).reshape(T, D)
         ids, gw = g4.moe_route(ctx, lg, K, True)
