@@ -271,7 +271,7 @@ class BatchedQ4_K(Workload):
         # splits summed by k_tok_reduce), its HALF form (token rows 8..15 not
         # loaded) up to eight tokens; the 16 q operands (SUB8) up to eight tokens and
         # from four row tiles per workgroup; whole slices and row tiles (FULL) here
-        self.dominant_name = ("k_rows<FmtQ4_K, 32, EPI_STORE>" if m <= 2 else
+        self.dominant_name = ("k_rows<FmtQ4_K, 32, EPI_STORE, KSEL>" if m <= 2 else
                               "k_tok_q4k<1, 16, true, %s, true> (bf16x3 MFMA 16x16x32)" % (
                                   "true, true" if m <= 8 else "false, true" if m > 16 else "false, false"))
         self.name = "q4_k_batched_8192x2048_m%d" % m
@@ -322,9 +322,10 @@ class MoeQ4_K(Workload):
             self.dominant_name = ("g4_moe_routed: k_route + k_grp_q4k<true> (gate+up rows) + k_gelu_mul4 + "
                                   "k_grp_q4k<true> (down) (experts grouped on the matrix cores) + k_moe_combine")
         else:
-            self.dominant_name = ("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE> (routing + gate_up) + " +
-                                  ("k_moe_down_xl<FmtQ4_K> (down + weighted sum)" if tokens == 1 else
-                                   "k_moe_down_xlt<FmtQ4_K> (down + weighted sum)"))
+            self.dominant_name = (("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE, KSEL> (routing + gate_up) + "
+                                   "k_moe_down_xl<FmtQ4_K> (down + weighted sum)") if tokens == 1 else
+                                  ("g4_moe_routed: k_rows<FmtQ4_K, 32, EPI_GELU_PAIR, ROUTE, 8 waves, SLOTW, KSEL> "
+                                   "(routing + gate_up) + k_moe_down_xlt<FmtQ4_K, STEP> (down + weighted sum)"))
         base = synth.moe_q4_k(tokens)
         E, D, FF, K = base["n_experts"], base["dim"], base["ff"], base["k"]
         self.E, self.D, self.FF, self.K = E, D, FF, K
