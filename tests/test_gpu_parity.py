@@ -560,9 +560,10 @@ def moe_slabs(g4, ctx, c):
     return _MOE_SLABS["w"]
 
 
-# the configured workload (128 experts, top-8, dim 2048, ff 1408): one token and
-# 16 tokens take the per-pair launches, 48 and 128 the expert-grouped ones
-@pytest.mark.parametrize("tokens", [1, 16, 48, 128])
+# the configured workload (128 experts, top-8, dim 2048, ff 1408): 1, 16 and 24
+# tokens take the per-pair launches (24: ten down row blocks of 26 row steps per
+# token, the last one partial), 48 and 128 the expert-grouped ones
+@pytest.mark.parametrize("tokens", [1, 16, 24, 48, 128])
 def test_moe_q4_k(g4, ctx, oracle, tokens):
     announce("workload moe q4_k T=%d" % tokens)
     c = synth.moe_q4_k(tokens)
